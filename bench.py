@@ -1,0 +1,248 @@
+"""Benchmark: fwd+bwd Expert-Threshold MoE dispatch/combine on one MI355X.
+
+One step = one pass of the path over one batch of synthetic input, inputs
+resident in HBM before timing starts:
+    route            threshold routing + CSR + permutation (3 kernels)
+    dispatch_fwd     Xp = permute(X)
+    combine_fwd      Y  = sum_s gate[s] * Yp[s]
+    combine_bwd      dYp = gate * dY[token], dgate = <dY, Yp>, dlogits (router grad)
+    dispatch_bwd     dX = sum_s dXp[s]
+Yp and dXp are separate resident buffers standing in for the expert FFN's
+output and input-gradient (the FFN itself is not part of the path).
+
+Metric: routed token-slots per second, and the step's algorithmic HBM bytes
+per second as a fraction of MI355X's 8 TB/s.  Workload: C3 (T=65536, d=4096,
+E=128, bf16, Zipf-skewed expert popularity) unless --workload says otherwise.
+
+Prints ONE JSON line on stdout (rank 0); a readable breakdown goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12   # MI355X HBM3E, bytes/s
+METRIC = "routed token-slots/sec fwd+bwd dispatch+combine; % of HBM peak (8 TB/s)"
+STAGES = ["route", "dispatch_fwd", "combine_fwd", "combine_bwd", "dispatch_bwd"]
+
+
+def algorithmic_bytes(T: int, E: int, S: int, d: int, b: int) -> dict:
+    """Minimum HBM bytes each stage must move (each element read or written once)."""
+    idx = 4
+    return {
+        # read logits once; write counts/offsets, token_offsets, 3 slot arrays
+        "route": T * E * 4 + (2 * E + 1) * idx + (T + 1) * idx + 3 * S * idx,
+        # read X, token_offsets, token_slot; write Xp
+        "dispatch_fwd": T * d * b + S * d * b + (T + 1) * idx + S * idx,
+        # read Yp, gates, token_offsets, token_slot; write Y
+        "combine_fwd": S * d * b + T * d * b + S * 4 + (T + 1) * idx + S * idx,
+        # read dY, Yp, gates, offsets, token_slot, expert_offsets; write dYp, dgate, dlogits
+        "combine_bwd": T * d * b + 2 * S * d * b + 2 * S * 4 + (T + 1) * idx + S * idx
+                       + (E + 1) * idx + T * E * 4,
+        # read dXp, offsets, token_slot; write dX
+        "dispatch_bwd": S * d * b + T * d * b + (T + 1) * idx + S * idx,
+    }
+
+
+def read_traffic(workload: str):
+    """Measured HBM bytes per combine_bwd launch, from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated), if one exists."""
+    path = os.path.join(ROOT, "profiles", f"pmc_combine_bwd_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
+    """The CPU restatement (oracle/, single thread) on the first `tokens`
+    tokens of the same workload, same ops as one GPU step."""
+    import numpy as np
+    import oracle
+    W = importlib.import_module("peer-review-agents_amd.workloads")
+    cfg = W.CONFIGS[workload]
+    lg, thr = W.router_inputs(workload, seed=seed)
+    lg = np.ascontiguousarray(lg[:tokens])
+    d, E = cfg["d"], cfg["E"]
+    r = oracle.route(lg, thr)
+    S = r.num_slots
+    conv = oracle.f32_to_bf16 if cfg["dtype"] == "bf16" else (lambda a: a)
+    x = conv(W.randn_rows(tokens, d, 1))
+    yp = conv(W.randn_rows(S, d, 2))
+    dy = conv(W.randn_rows(tokens, d, 3, 0.02))
+    dxp = conv(W.randn_rows(S, d, 4))
+    t0 = time.perf_counter()
+    r = oracle.route(lg, thr)
+    oracle.dispatch_fwd(x, r)
+    oracle.combine_fwd(yp, r, tokens)
+    oracle.combine_bwd(dy, yp, r, E, want_dlogits=True)
+    oracle.dispatch_bwd(dxp, r, tokens)
+    dt = time.perf_counter() - t0
+    return {"value": S / dt, "unit": "slots/s", "cores": 1, "kind": "port",
+            "sample": f"first {tokens} of {cfg['T']} tokens of {workload} ({S} slots), "
+                      f"one fwd+bwd pass, single thread, {dt:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-tokens", type=int, default=8192,
+                    help="tokens in the CPU baseline's sample (0 skips it)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs the path on one GPU's "
+              "local share of experts and has no multi-GPU (expert-parallel) mode; "
+              "run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    et = importlib.import_module("peer-review-agents_amd")
+    W = importlib.import_module("peer-review-agents_amd.workloads")
+    lib = et.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = W.CONFIGS[args.workload]
+    T, d, E = cfg["T"], cfg["d"], cfg["E"]
+    act = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    b = 2 if act == torch.bfloat16 else 4
+    dt_code = 1 if act == torch.bfloat16 else 0
+
+    # ---- resident inputs ------------------------------------------------------
+    lg_h, thr_h = W.router_inputs(args.workload, seed=args.seed)
+    logits = torch.from_numpy(lg_h).to(dev)
+    thr = torch.from_numpy(thr_h).to(dev)
+    plan = et.route(logits, thr)                 # sizes the slot buffers (one sync, untimed)
+    S = plan.num_slots
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    X = torch.randn(T, d, device=dev, generator=g).to(act)
+    YP = torch.randn(S, d, device=dev, generator=g).to(act)
+    DY = (torch.randn(T, d, device=dev, generator=g) * 0.02).to(act)
+    DXP = torch.randn(S, d, device=dev, generator=g).to(act)
+    i32 = dict(dtype=torch.int32, device=dev)
+    counts, eoff, toff = torch.empty(E, **i32), torch.empty(E + 1, **i32), torch.empty(T + 1, **i32)
+    st, ts = torch.empty(S, **i32), torch.empty(S, **i32)
+    sg = torch.empty(S, dtype=torch.float32, device=dev)
+    wsb = et.route_workspace_bytes(T, E)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    XP = torch.empty(S, d, dtype=act, device=dev)
+    Y = torch.empty(T, d, dtype=act, device=dev)
+    DYP = torch.empty(S, d, dtype=act, device=dev)
+    DGATE = torch.empty(S, dtype=torch.float32, device=dev)
+    DL = torch.empty(T, E, dtype=torch.float32, device=dev)
+    DX = torch.empty(T, d, dtype=act, device=dev)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = [vp(t) for t in (logits, thr, counts, eoff, toff, st, sg, ts, ws, X, XP, YP, Y, DY, DYP, DGATE, DL,
+                         DXP, DX)]
+    (p_lg, p_thr, p_cnt, p_eo, p_to, p_st, p_sg, p_ts, p_ws, p_x, p_xp, p_yp, p_y, p_dy, p_dyp, p_dg, p_dl,
+     p_dxp, p_dx) = P
+
+    def stage(i):
+        if i == 0:
+            rc = lib.et_route(p_lg, p_thr, T, E, p_cnt, p_eo, p_to, p_st, p_sg, p_ts, S, p_ws, wsb, sp)
+        elif i == 1:
+            rc = lib.et_dispatch_fwd(p_x, T, d, dt_code, p_to, p_ts, S, p_xp, sp)
+        elif i == 2:
+            rc = lib.et_combine_fwd(p_yp, p_sg, p_to, p_ts, T, d, dt_code, S, p_y, sp)
+        elif i == 3:
+            rc = lib.et_combine_bwd(p_dy, p_yp, p_sg, p_to, p_ts, p_eo, T, E, d, dt_code, S, p_dyp, p_dg, p_dl, sp)
+        else:
+            rc = lib.et_dispatch_bwd(p_dxp, p_to, p_ts, T, d, dt_code, S, p_dx, sp)
+        if rc != 0:
+            raise RuntimeError(f"stage {STAGES[i]} failed: {lib.et_last_error().decode()}")
+
+    for _ in range(args.warmup):
+        for i in range(len(STAGES)):
+            stage(i)
+    torch.cuda.synchronize()
+    assert int(eoff[E]) == S, "routing changed between runs"
+
+    # ---- timed region -----------------------------------------------------------
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        ev[k][0].record(stream)
+        for i in range(len(STAGES)):
+            stage(i)
+            ev[k][i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    stage_ms = {name: 0.0 for name in STAGES}
+    for k in range(args.steps):
+        for i, name in enumerate(STAGES):
+            stage_ms[name] += ev[k][i].elapsed_time(ev[k][i + 1]) / args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    abytes = algorithmic_bytes(T, E, S, d, b)
+    step_bytes = sum(abytes.values())
+    kernels = {}
+    for name in STAGES:
+        gbs = abytes[name] / (stage_ms[name] * 1e-3) / 1e9
+        kernels[name] = {"ms": round(stage_ms[name], 4), "GB/s": round(gbs, 1),
+                         "frac": round(gbs * 1e9 / HBM_PEAK, 4), "bytes": abytes[name]}
+    dom = "combine_bwd"
+    ach = abytes[dom] / (stage_ms[dom] * 1e-3) / 1e9
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4),
+                "traffic": read_traffic(args.workload), "algorithmic_bytes": abytes[dom]}
+
+    cpu = None
+    if args.cpu_tokens > 0:
+        cpu = cpu_baseline(args.workload, args.seed, min(args.cpu_tokens, T))
+
+    slots_per_s = S / (ms_per_step * 1e-3)
+    out = {
+        "metric": METRIC,
+        "value": round(slots_per_s, 1),
+        "unit": "slots/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: T={T} d={d} E={E} {cfg['dtype']}, "
+                               f"thresholds {cfg['thr']}", "T": T, "d": d, "E": E, "slots": S,
+                   "mean_k": round(S / T, 4), "seed": args.seed, "parallelism": "single GPU"},
+        "hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / HBM_PEAK, 4),
+        "step_bytes": step_bytes,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    for name in STAGES:
+        k = kernels[name]
+        print(f"  {name:13s} {k['ms']:8.4f} ms  {k['GB/s']:8.1f} GB/s  {100 * k['frac']:5.1f}% of peak",
+              file=sys.stderr)
+    print(f"  step {ms_per_step:.4f} ms, {slots_per_s / 1e6:.2f} M slots/s, "
+          f"{100 * out['hbm_frac']:.1f}% of HBM peak", file=sys.stderr)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

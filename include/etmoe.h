@@ -1,0 +1,157 @@
+/*
+ * etmoe.h -- C ABI of the MI355X (gfx950) Expert-Threshold MoE token-dispatch
+ * library, libetmoe.so.
+ *
+ * The path: per-expert threshold routing on sigmoid router scores with a
+ * zero-expert fallback to argmax, an EMA threshold update, a histogram +
+ * exclusive-scan CSR of expert offsets, a stable permutation of tokens into
+ * expert-major slots (ordered by expert, then token id), the gate-weighted
+ * un-permute ("combine"), and the backward of both (dX, dYp, dgate, and the
+ * router-logit gradient).
+ *
+ * Reference interface.  The reference tree (bat0001/peer-review-agents) holds
+ * no operator, plugin or FFI interface for this path -- its only extension
+ * points are an agent-backend registry (cli/reva/backends.py:28-131) and a
+ * log-translator table (cli/reva/translators/__init__.py:33-53).  So no entry
+ * point below replaces a reference symbol; each says which step of the path it
+ * implements, and the signatures are this library's own.
+ *
+ * Conventions (all entry points):
+ *  - Every pointer argument is a DEVICE pointer unless its comment says
+ *    otherwise.  Arrays are dense and row-major; activations have row stride d.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Calls only
+ *    enqueue work; they never synchronise the stream and never allocate.
+ *  - Return 0 on success, a negative ET_ERR_* code otherwise; et_last_error()
+ *    then describes the failure (thread-local, valid until the next call on the
+ *    same host thread).  Argument errors are detected before anything is
+ *    enqueued.
+ *  - Index arrays are int32: T*E must stay below 2^31.
+ *  - `slot_capacity` is the allocated length of the slot arrays (sorted_token,
+ *    slot_gate, token_slot, dgate) and the row count of the slot-major
+ *    activation buffers (Xp, Yp, dYp, dXp).  Routing never writes a slot index
+ *    >= slot_capacity, and the row kernels skip such slots, so an undersized
+ *    buffer loses data but is never written out of bounds.  T*E is always a
+ *    sufficient capacity.  The number of routed slots S is expert_offsets[E]
+ *    (also token_offsets[T]); compare it with the capacity after routing.
+ *  - Concurrent calls on different streams are safe when their buffers are
+ *    disjoint (the library keeps no device state).
+ */
+#ifndef ETMOE_H
+#define ETMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ET_ABI_VERSION 1
+
+/* activation dtypes */
+#define ET_DTYPE_F32 0
+#define ET_DTYPE_BF16 1
+
+/* status codes */
+#define ET_OK 0
+#define ET_ERR_INVALID_ARGUMENT -1
+#define ET_ERR_WORKSPACE_TOO_SMALL -2
+#define ET_ERR_LAUNCH -3
+#define ET_ERR_UNSUPPORTED -4
+
+/* Largest expert count the routing kernels accept. */
+#define ET_MAX_EXPERTS 1024
+
+int et_abi_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* et_last_error(void);
+
+/* Bytes of device workspace et_route needs for T tokens and E experts. */
+size_t et_route_workspace_bytes(int64_t num_tokens, int64_t num_experts);
+
+/*
+ * Routing: threshold selection + histogram/scan CSR + stable permutation.
+ *   logits         f32 [T, E]  router logits; score = sigmoid(logit)
+ *   thr            f32 [E]     per-expert thresholds
+ * Selection: (t, e) is routed iff score[t,e] >= thr[e]; a token with no such
+ * expert is routed to argmax_e score[t,e] (NaN lowest, ties to the lowest e).
+ * Outputs:
+ *   counts         i32 [E]     tokens per expert
+ *   expert_offsets i32 [E+1]   exclusive scan of counts (expert_offsets[E] = S)
+ *   token_offsets  i32 [T+1]   exclusive scan of per-token expert counts
+ *   sorted_token   i32 [cap]   slot -> token id, slots ordered by (expert, token)
+ *   slot_gate      f32 [cap]   gate of each slot = its sigmoid score
+ *   token_slot     i32 [cap]   token-major slot lists, ascending expert
+ * Deterministic and atomics-free: repeated calls give identical bits.
+ * Implements the routing step of the path (no reference counterpart).
+ */
+int et_route(const float* logits, const float* thr, int64_t num_tokens, int64_t num_experts,
+             int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+             int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+             int64_t slot_capacity, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Dispatch (permute / scatter) forward:  Xp[slot, :] = X[token(slot), :].
+ *   x  [T, d] of `dtype`,  xp [cap, d] of `dtype`.  Exact row copies.
+ * Implements the dispatch step of the path (no reference counterpart).
+ */
+int et_dispatch_fwd(const void* x, int64_t num_tokens, int64_t d, int dtype,
+                    const int32_t* token_offsets, const int32_t* token_slot,
+                    int64_t slot_capacity, void* xp, void* stream);
+
+/*
+ * Combine (un-permute / gather) forward:
+ *   Y[t, c] = cast(acc), acc = 0; for t's slots s in ascending expert order:
+ *             acc = fma(slot_gate[s], Yp[s, c], acc)      (binary32)
+ *   yp [cap, d], y [T, d] of `dtype`.  Bit-exact with that definition.
+ * Implements the combine step of the path (no reference counterpart).
+ */
+int et_combine_fwd(const void* yp, const float* slot_gate, const int32_t* token_offsets,
+                   const int32_t* token_slot, int64_t num_tokens, int64_t d, int dtype,
+                   int64_t slot_capacity, void* y, void* stream);
+
+/*
+ * Combine backward (fused): for every slot s of token t = token(s), expert e:
+ *   dYp[s, c]     = cast(slot_gate[s] * dY[t, c])
+ *   dgate[s]      = sum_c dY[t, c] * Yp[s, c]            (binary32 accumulate)
+ *   dlogits[t, e] = dgate[s] * g * (1 - g), g = slot_gate[s]; 0 elsewhere
+ * dlogits (f32 [T, E]) may be NULL; expert_offsets is read only when it is not.
+ * Implements the combine backward of the path (no reference counterpart).
+ */
+int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
+                   const int32_t* token_offsets, const int32_t* token_slot,
+                   const int32_t* expert_offsets, int64_t num_tokens, int64_t num_experts,
+                   int64_t d, int dtype, int64_t slot_capacity,
+                   void* dyp, float* dgate, float* dlogits, void* stream);
+
+/*
+ * Dispatch backward:  dX[t, c] = cast(sum of dXp[s, c] over t's slots, added in
+ * ascending expert order in binary32).  dxp [cap, d], dx [T, d] of `dtype`.
+ * Implements the dispatch backward of the path (no reference counterpart).
+ */
+int et_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
+                    int64_t num_tokens, int64_t d, int dtype, int64_t slot_capacity,
+                    void* dx, void* stream);
+
+/* Bytes of device workspace et_threshold_update needs for E experts. */
+size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
+
+/*
+ * EMA threshold update, in place on thr (f32 [E]):
+ *   stat[e] = the c-th largest score of expert e's column, c = ceil(T*k/E)
+ *             clamped to [1, T] (NaN scores order as 0)
+ *   thr[e]  = fma(momentum, thr[e], (1 - momentum) * stat[e])
+ * stat (f32 [E]) may be NULL.  T == 0 leaves thr unchanged.  Exact selection
+ * (radix select on the score bits), so thr is bit-exact with the definition.
+ * Implements the EMA threshold update of the path (no reference counterpart).
+ */
+int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int64_t num_experts,
+                        int64_t k_target, float momentum, float* stat,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ETMOE_H */

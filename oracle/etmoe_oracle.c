@@ -1,0 +1,323 @@
+/*
+ * etmoe_oracle.c -- CPU restatement of the Expert-Threshold MoE token-dispatch
+ * specification.  TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * this library, and only as the checker (or, in bench.py, as the timed CPU
+ * baseline).  The product path (the HIP library under peer-review-agents_amd/)
+ * never links, loads or falls back to it.
+ *
+ * Provenance.  The mounted reference tree (bat0001/peer-review-agents) contains
+ * no routing, CSR, permutation or combine code in any language: it is a Python
+ * CLI that launches LLM reviewing agents (cli/reva/cli.py:40-536,
+ * cli/reva/tmux.py:171-260).  There is therefore no reference file:line for any
+ * function below.  Every function restates the written specification of the
+ * path (threshold routing on sigmoid scores, EMA threshold update, zero-expert
+ * fallback to argmax, histogram + exclusive-scan CSR, stable permutation by
+ * (expert, token id), gate-weighted combine, and their backward), with each
+ * open choice fixed explicitly in the comment of the function that makes it.
+ * Parity against the reference is UNPINNED for every function: the reference
+ * holds no golden vectors, fixtures or CPU path for it.  Each function is
+ * pinned instead against independent mathematics in tests/test_oracle.py
+ * (library stable sort, bincount/cumsum, brute force, float64 autograd,
+ * double-precision exp, EMA closed form, hand-derived known answers).
+ *
+ * Floating point: build with -ffp-contract=off.  fmaf() is used exactly where
+ * the specification says "fused multiply-add"; every other + - * / is a single
+ * IEEE binary32 operation with round-to-nearest-even.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define OR_DT_F32 0
+#define OR_DT_BF16 1
+
+/* ------------------------------------------------------------------------ */
+/* binary32 <-> bfloat16                                                    */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* Round-to-nearest-even truncation of the low 16 bits.  A NaN keeps its sign
+ * and top payload bits and is forced quiet (bit 6 of the bf16 word). */
+uint16_t oracle_f32_to_bf16(float f)
+{
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f(((uint32_t)h) << 16); }
+
+static inline float load_elem(const void* base, int64_t i, int dt)
+{
+    if (dt == OR_DT_BF16) return oracle_bf16_to_f32(((const uint16_t*)base)[i]);
+    return ((const float*)base)[i];
+}
+
+static inline void store_elem(void* base, int64_t i, float v, int dt)
+{
+    if (dt == OR_DT_BF16) ((uint16_t*)base)[i] = oracle_f32_to_bf16(v);
+    else ((float*)base)[i] = v;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Score: sigmoid with a fully specified exp                                */
+/* ------------------------------------------------------------------------ */
+
+/* exp(x) for x <= 0, specified operation by operation so that any IEEE
+ * binary32 machine with a correctly rounded fma reproduces it bit for bit.
+ * Method: Cody-Waite reduction x = n*ln2 + r with n = rint(x*log2(e)) and ln2
+ * split into a 16-bit-exact high part and a low part, then the degree-7
+ * Taylor polynomial of exp(r) on |r| <= ln2/2 in Horner form, then scaling by
+ * 2^n built from the exponent field.  Inputs below -87 return 0 (exp(-87) is
+ * 1.6e-38, the bottom of the normal range), so no subnormal is produced. */
+float oracle_exp_nonpos(float x)
+{
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    const float log2e = 1.4426950216293335f;   /* 0x3FB8AA3B */
+    const float ln2_hi = 0.693145751953125f;        /* 0x3F317200 */
+    const float ln2_lo = 1.428606765330187e-6f; /* 0x35BFBE8E */
+    float n = rintf(x * log2e);
+    float r = fmaf(-n, ln2_hi, x);
+    r = fmaf(-n, ln2_lo, r);
+    float p = 1.9841270113829523e-4f;  /* 1/5040, 0x39500D01 */
+    p = fmaf(p, r, 1.3888889225199819e-3f);   /* 1/720, 0x3AB60B61 */
+    p = fmaf(p, r, 8.333333767950535e-3f);    /* 1/120, 0x3C088889 */
+    p = fmaf(p, r, 4.16666679084301e-2f);     /* 1/24,  0x3D2AAAAB */
+    p = fmaf(p, r, 1.666666716337204e-1f);    /* 1/6,   0x3E2AAAAB */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ni = (int)n;                   /* -126 <= ni <= 0 */
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* score = sigmoid(l).  l >= 0: 1 / (1 + exp(-l));  l < 0: exp(l) / (1 + exp(l)).
+ * NaN propagates; +inf -> 1, -inf -> 0. */
+float oracle_sigmoid(float l)
+{
+    if (l != l) return l;
+    if (l >= 0.0f) {
+        float z = oracle_exp_nonpos(-l);
+        return 1.0f / (1.0f + z);
+    }
+    float z = oracle_exp_nonpos(l);
+    return z / (1.0f + z);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Routing: threshold selection, fallback, CSR by expert, CSR by token       */
+/* ------------------------------------------------------------------------ */
+
+/* Selection rule (written once, used by route and by the tests):
+ *   sel[t,e] = score[t,e] >= thr[e]            (a NaN score or thr never selects)
+ *   if no expert is selected for token t, sel[t,e*] = 1 with
+ *   e* = argmax_e score[t,e], NaN counted below every number, ties to the
+ *   lowest expert index, and e* = 0 when every score is NaN.
+ * Fills sel (T*E bytes) and score (T*E floats); returns S = sum of sel. */
+int64_t oracle_select(const float* logits, const float* thr, int64_t T, int64_t E,
+                      uint8_t* sel, float* score)
+{
+    int64_t S = 0;
+    for (int64_t t = 0; t < T; ++t) {
+        int64_t k = 0;
+        for (int64_t e = 0; e < E; ++e) {
+            float s = oracle_sigmoid(logits[t * E + e]);
+            score[t * E + e] = s;
+            uint8_t on = (s >= thr[e]) ? 1 : 0;
+            sel[t * E + e] = on;
+            k += on;
+        }
+        if (k == 0 && E > 0) {
+            int64_t best = 0;
+            float bv = -1.0f;              /* every valid score is >= 0 */
+            for (int64_t e = 0; e < E; ++e) {
+                float s = score[t * E + e];
+                float v = (s != s) ? -1.0f : s;
+                if (v > bv) { bv = v; best = e; }
+            }
+            sel[t * E + best] = 1;
+            k = 1;
+        }
+        S += k;
+    }
+    return S;
+}
+
+/* Full routing.  Outputs (int32 unless noted):
+ *   counts[E]            tokens routed to each expert (histogram)
+ *   expert_offsets[E+1]  exclusive prefix sum of counts; expert_offsets[E] = S
+ *   token_offsets[T+1]   exclusive prefix sum of k_t; token_offsets[T] = S
+ *   sorted_token[S]      slot -> token id; slots ordered by (expert, token id),
+ *                        i.e. a stable sort of the selected (t,e) pairs by e
+ *   slot_gate[S] (f32)   gate of the slot = score[t,e] (raw sigmoid score)
+ *   token_slot[S]        token-major slot list: for token t, its slots in
+ *                        ascending expert order at token_offsets[t]..
+ * Slot arrays are written only for indices < slot_capacity.  Returns S, or -1
+ * if scratch allocation fails. */
+int64_t oracle_route(const float* logits, const float* thr, int64_t T, int64_t E,
+                     int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                     int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                     int64_t slot_capacity)
+{
+    size_t n = (size_t)(T * E);
+    uint8_t* sel = (uint8_t*)malloc(n ? n : 1);
+    float* score = (float*)malloc((n ? n : 1) * sizeof(float));
+    int32_t* slot_of = (int32_t*)malloc((n ? n : 1) * sizeof(int32_t));
+    if (!sel || !score || !slot_of) { free(sel); free(score); free(slot_of); return -1; }
+
+    int64_t S = oracle_select(logits, thr, T, E, sel, score);
+
+    /* histogram */
+    for (int64_t e = 0; e < E; ++e) counts[e] = 0;
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t e = 0; e < E; ++e) counts[e] += sel[t * E + e];
+    /* exclusive scan */
+    expert_offsets[0] = 0;
+    for (int64_t e = 0; e < E; ++e) expert_offsets[e + 1] = expert_offsets[e] + counts[e];
+
+    /* slots in (expert, token) lexicographic order */
+    int64_t s = 0;
+    for (int64_t e = 0; e < E; ++e)
+        for (int64_t t = 0; t < T; ++t) {
+            if (!sel[t * E + e]) continue;
+            slot_of[t * E + e] = (int32_t)s;
+            if (s < slot_capacity) {
+                sorted_token[s] = (int32_t)t;
+                slot_gate[s] = score[t * E + e];
+            }
+            ++s;
+        }
+
+    /* token-major CSR */
+    int64_t pos = 0;
+    for (int64_t t = 0; t < T; ++t) {
+        token_offsets[t] = (int32_t)pos;
+        for (int64_t e = 0; e < E; ++e) {
+            if (!sel[t * E + e]) continue;
+            if (pos < slot_capacity) token_slot[pos] = slot_of[t * E + e];
+            ++pos;
+        }
+    }
+    token_offsets[T] = (int32_t)pos;
+
+    free(sel); free(score); free(slot_of);
+    return S;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dispatch (permute) and combine (un-permute), forward and backward         */
+/* ------------------------------------------------------------------------ */
+
+/* Xp[slot(t,e), :] = X[t, :] -- an exact row copy (dtype-agnostic). */
+void oracle_dispatch_fwd(const void* x, int64_t T, int64_t d, int dt,
+                         const int32_t* token_offsets, const int32_t* token_slot, void* xp)
+{
+    size_t row = (size_t)d * (dt == OR_DT_BF16 ? 2 : 4);
+    for (int64_t t = 0; t < T; ++t)
+        for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j)
+            memcpy((char*)xp + (size_t)token_slot[j] * row, (const char*)x + (size_t)t * row, row);
+}
+
+/* Y[t,c] = cast(acc), acc = 0; for each slot s of t in ascending expert order:
+ * acc = fmaf(gate[s], Yp[s,c], acc).  With gate == NULL every gate is 1 and the
+ * fma is the plain sum acc + Yp[s,c] (fmaf(1, y, acc) rounds exactly like it);
+ * that is the backward of dispatch, dX[t,:] = sum of dXp over t's slots. */
+void oracle_combine_fwd(const void* yp, const float* gate, const int32_t* token_offsets,
+                        const int32_t* token_slot, int64_t T, int64_t d, int dt, void* y)
+{
+    float* acc = (float*)malloc((size_t)(d ? d : 1) * sizeof(float));
+    for (int64_t t = 0; t < T; ++t) {
+        for (int64_t c = 0; c < d; ++c) acc[c] = 0.0f;
+        for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j) {
+            int64_t s = token_slot[j];
+            float g = gate ? gate[s] : 1.0f;
+            for (int64_t c = 0; c < d; ++c) acc[c] = fmaf(g, load_elem(yp, s * d + c, dt), acc[c]);
+        }
+        for (int64_t c = 0; c < d; ++c) store_elem(y, t * d + c, acc[c], dt);
+    }
+    free(acc);
+}
+
+void oracle_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
+                         int64_t T, int64_t d, int dt, void* dx)
+{
+    oracle_combine_fwd(dxp, NULL, token_offsets, token_slot, T, d, dt, dx);
+}
+
+/* Backward of combine for slot s (token t = sorted_token[s], expert e):
+ *   dYp[s,c]   = cast(gate[s] * dY[t,c])       one binary32 multiply, then cast
+ *   dgate[s]   = sum_c dY[t,c] * Yp[s,c]        (accumulated here in double; the
+ *                                               product path may use any order)
+ *   dlogits[t,e] = dgate[s] * g * (1 - g), g = gate[s]   (selected pairs)
+ *   dlogits[t,e] = 0                                      (all other pairs)
+ * dlogits may be NULL. */
+void oracle_combine_bwd(const void* dy, const void* yp, const float* gate,
+                        const int32_t* sorted_token, const int32_t* expert_offsets,
+                        int64_t T, int64_t E, int64_t d, int dt,
+                        void* dyp, float* dgate, float* dlogits)
+{
+    if (dlogits) for (int64_t i = 0; i < T * E; ++i) dlogits[i] = 0.0f;
+    for (int64_t e = 0; e < E; ++e)
+        for (int64_t s = expert_offsets[e]; s < expert_offsets[e + 1]; ++s) {
+            int64_t t = sorted_token[s];
+            double dot = 0.0;
+            for (int64_t c = 0; c < d; ++c) {
+                float g_dy = load_elem(dy, t * d + c, dt);
+                dot += (double)g_dy * (double)load_elem(yp, s * d + c, dt);
+                store_elem(dyp, s * d + c, gate[s] * g_dy, dt);
+            }
+            dgate[s] = (float)dot;
+            if (dlogits) {
+                double g = gate[s];
+                dlogits[t * E + e] = (float)(dot * (g * (1.0 - g)));
+            }
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* EMA threshold update                                                     */
+/* ------------------------------------------------------------------------ */
+
+static int cmp_u32_desc(const void* a, const void* b)
+{
+    uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+    return (x < y) - (x > y);
+}
+
+/* Per-expert statistic: the c-th largest score of the expert's column, with
+ * c = ceil(T * k_target / E) clamped to [1, T] (the capacity an expert would
+ * take under expert-choice routing at k_target experts per token).  Scores
+ * are ordered by their bit pattern (all scores are >= 0, so this is numeric
+ * order); a NaN score orders as 0.0.  Update, in this order of operations:
+ *     thr[e] = fmaf(m, thr[e], (1 - m) * stat[e])
+ * T == 0 leaves thr and stat untouched.  stat may be NULL.  Returns c, or -1
+ * if scratch allocation fails. */
+int64_t oracle_threshold_update(const float* logits, float* thr, int64_t T, int64_t E,
+                                int64_t k_target, float momentum, float* stat)
+{
+    if (T <= 0) return 0;
+    int64_t c = (T * k_target + E - 1) / E;
+    if (c < 1) c = 1;
+    if (c > T) c = T;
+    uint32_t* keys = (uint32_t*)malloc((size_t)T * sizeof(uint32_t));
+    if (!keys) return -1;
+    for (int64_t e = 0; e < E; ++e) {
+        for (int64_t t = 0; t < T; ++t) {
+            float s = oracle_sigmoid(logits[t * E + e]);
+            keys[t] = (s != s) ? 0u : f2u(s);
+        }
+        qsort(keys, (size_t)T, sizeof(uint32_t), cmp_u32_desc);
+        float st = u2f(keys[c - 1]);
+        if (stat) stat[e] = st;
+        thr[e] = fmaf(momentum, thr[e], (1.0f - momentum) * st);
+    }
+    free(keys);
+    return c;
+}

@@ -1,0 +1,21 @@
+"""MI355X-native (gfx950) Expert-Threshold MoE token-dispatch path.
+
+Import with ``importlib.import_module("peer-review-agents_amd")`` (the
+directory name is not a Python identifier).  Kernels live in csrc/ and are
+built into libetmoe.so by build.py; the host API is in expert_threshold.py.
+"""
+from ._lib import ETMoEError, LIB_PATH, header_symbols, lib  # noqa: F401
+from .expert_threshold import (  # noqa: F401
+    ExpertThresholdRouter,
+    RoutingPlan,
+    combine,
+    combine_autograd,
+    combine_backward,
+    dispatch,
+    dispatch_autograd,
+    dispatch_backward,
+    route,
+    route_workspace_bytes,
+    threshold_update_,
+    threshold_workspace_bytes,
+)

@@ -1,0 +1,132 @@
+// et_common.hpp -- device helpers shared by the routing and row kernels of
+// libetmoe.so (gfx950, wave64).  Also the host-side error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "etmoe.h"
+
+namespace et {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// host-side status plumbing
+// ---------------------------------------------------------------------------
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+// Returns ET_OK, or ET_ERR_LAUNCH with the HIP error text recorded.
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------
+// bit casts and bf16
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// bf16 -> f32 is a 16-bit shift of the word.
+__device__ __forceinline__ float bf16lo(uint32_t w) { return u2f(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return u2f(w & 0xffff0000u); }
+
+// f32 -> bf16, round to nearest even; a NaN keeps sign and top payload and is
+// forced quiet.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
+{
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x0040u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// specified exp / sigmoid (bit-exact on any IEEE binary32 machine with fma)
+// ---------------------------------------------------------------------------
+
+// exp(x) for x <= 0: Cody-Waite reduction with n = rint(x*log2 e), ln2 split
+// into an exact high part and a low part, degree-7 Taylor polynomial of exp(r)
+// on |r| <= ln2/2 in Horner form with fma, scaled by 2^n through the exponent
+// field.  x < -87 gives 0, so no result is subnormal.
+__device__ __forceinline__ float exp_nonpos(float x)
+{
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    const float log2e = 1.4426950216293335f;     // 0x3FB8AA3B
+    const float ln2_hi = 0.693145751953125f;     // 0x3F317200
+    const float ln2_lo = 1.428606765330187e-6f;  // 0x35BFBE8E
+    float n = __builtin_rintf(x * log2e);
+    float r = __builtin_fmaf(-n, ln2_hi, x);
+    r = __builtin_fmaf(-n, ln2_lo, r);
+    float p = 1.9841270113829523e-4f;
+    p = __builtin_fmaf(p, r, 1.3888889225199819e-3f);
+    p = __builtin_fmaf(p, r, 8.333333767950535e-3f);
+    p = __builtin_fmaf(p, r, 4.16666679084301e-2f);
+    p = __builtin_fmaf(p, r, 1.666666716337204e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    int ni = (int)n;
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+// sigmoid(l): l >= 0 -> 1/(1+exp(-l)); l < 0 -> exp(l)/(1+exp(l)); NaN stays NaN.
+// Both divisions are IEEE correctly rounded (HIP's default for binary32).
+__device__ __forceinline__ float sigmoid(float l)
+{
+    if (l != l) return l;
+    if (l >= 0.0f) {
+        float z = exp_nonpos(-l);
+        return 1.0f / (1.0f + z);
+    }
+    float z = exp_nonpos(l);
+    return z / (1.0f + z);
+}
+
+// ---------------------------------------------------------------------------
+// wave helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+// popcount(mask & lanes-below-me)
+__device__ __forceinline__ int rank_below(uint64_t mask)
+{
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Inclusive prefix sum across the wave.
+__device__ __forceinline__ int wave_incl_scan(int v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        int o = __shfl_up(v, off, kWave);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+}  // namespace et

@@ -1,0 +1,540 @@
+// et_rows.hip -- the row-moving kernels of the path on gfx950: dispatch
+// (permute), combine (gate-weighted un-permute), combine backward (dYp, dgate,
+// dlogits) and dispatch backward (dX).
+//
+// All four are token-major: one wave owns one token, reads its slot list
+// token_slot[token_offsets[t] .. token_offsets[t+1]) once, and moves whole
+// rows.  Token-major order is what makes the traffic minimal: X and dY rows
+// are read exactly once (then written or consumed k_t times from registers),
+// Y and dX rows are written exactly once, and sums over a token's slots are
+// formed in registers in ascending expert order without atomics.
+//
+// Vector path: rows whose byte size is a multiple of 16 move as 16-byte
+// chunks, 64 lanes x 16 B = 1 KiB per wave instruction (fully coalesced), PCH
+// chunks per lane per pass over the row.  Other rows take the element path.
+#include "et_common.hpp"
+
+namespace et {
+
+constexpr int kRowWaves = 4;
+constexpr int kRowThreads = kRowWaves * kWave;
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4u ld16(const char* p) { return *reinterpret_cast<const v4u*>(p); }
+__device__ __forceinline__ void st16(char* p, v4u v) { *reinterpret_cast<v4u*>(p) = v; }
+
+template <int DT> struct Pack;
+
+template <> struct Pack<ET_DTYPE_F32> {
+    static constexpr int N = 4;
+    __device__ static __forceinline__ void unpack(v4u w, float* f)
+    {
+        f[0] = u2f(w.x); f[1] = u2f(w.y); f[2] = u2f(w.z); f[3] = u2f(w.w);
+    }
+    __device__ static __forceinline__ v4u pack(const float* f)
+    {
+        v4u w;
+        w.x = f2u(f[0]); w.y = f2u(f[1]); w.z = f2u(f[2]); w.w = f2u(f[3]);
+        return w;
+    }
+};
+
+template <> struct Pack<ET_DTYPE_BF16> {
+    static constexpr int N = 8;
+    __device__ static __forceinline__ void unpack(v4u w, float* f)
+    {
+        f[0] = bf16lo(w.x); f[1] = bf16hi(w.x); f[2] = bf16lo(w.y); f[3] = bf16hi(w.y);
+        f[4] = bf16lo(w.z); f[5] = bf16hi(w.z); f[6] = bf16lo(w.w); f[7] = bf16hi(w.w);
+    }
+    __device__ static __forceinline__ v4u pack(const float* f)
+    {
+        v4u w;
+        w.x = pack_bf16x2(f[0], f[1]); w.y = pack_bf16x2(f[2], f[3]);
+        w.z = pack_bf16x2(f[4], f[5]); w.w = pack_bf16x2(f[6], f[7]);
+        return w;
+    }
+};
+
+template <int DT> __device__ __forceinline__ float load_elem(const char* base, int64_t i);
+template <> __device__ __forceinline__ float load_elem<ET_DTYPE_F32>(const char* base, int64_t i)
+{
+    return reinterpret_cast<const float*>(base)[i];
+}
+template <> __device__ __forceinline__ float load_elem<ET_DTYPE_BF16>(const char* base, int64_t i)
+{
+    return u2f(uint32_t(reinterpret_cast<const uint16_t*>(base)[i]) << 16);
+}
+template <int DT> __device__ __forceinline__ void store_elem(char* base, int64_t i, float v);
+template <> __device__ __forceinline__ void store_elem<ET_DTYPE_F32>(char* base, int64_t i, float v)
+{
+    reinterpret_cast<float*>(base)[i] = v;
+}
+template <> __device__ __forceinline__ void store_elem<ET_DTYPE_BF16>(char* base, int64_t i, float v)
+{
+    reinterpret_cast<uint16_t*>(base)[i] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+// Wave-uniform token id and the clamped range of its slot-list entries.
+struct TokenSpan {
+    int t;
+    int j0, j1;
+};
+
+__device__ __forceinline__ bool token_span(int T, const int32_t* __restrict__ tok_off, int64_t cap,
+                                           TokenSpan& sp)
+{
+    sp.t = (int)blockIdx.x * kRowWaves + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    if (sp.t >= T) return false;
+    const int64_t a = tok_off[sp.t];
+    const int64_t b = tok_off[sp.t + 1];
+    sp.j0 = (int)min(a, cap);
+    sp.j1 = (int)max(min(b, cap), (int64_t)sp.j0);
+    return true;
+}
+
+// The u-th entry of the 64-entry block of the slot list starting at jb: each
+// lane loads one entry, then entries are broadcast with readlane.
+__device__ __forceinline__ int load_slot_block(const int32_t* __restrict__ tok_slot, int jb, int j1)
+{
+    const int j = jb + lane_id();
+    return j < j1 ? tok_slot[j] : -1;
+}
+
+// ---------------------------------------------------------------------------
+// dispatch forward: Xp[s] = X[t] for each slot s of t
+// ---------------------------------------------------------------------------
+
+template <int PCH>
+__global__ __launch_bounds__(kRowThreads) void dispatch_fwd_vec(
+    const char* __restrict__ x, int T, int64_t nch, const int32_t* __restrict__ tok_off,
+    const int32_t* __restrict__ tok_slot, int64_t cap, char* __restrict__ xp)
+{
+    TokenSpan sp;
+    if (!token_span(T, tok_off, cap, sp)) return;
+    const int lane = lane_id();
+    const int64_t rb = nch * 16;
+    const char* xrow = x + (int64_t)sp.t * rb;
+    for (int64_t c0 = 0; c0 < nch; c0 += PCH * kWave) {
+        v4u v[PCH];
+#pragma unroll
+        for (int q = 0; q < PCH; ++q) {
+            const int64_t idx = c0 + q * kWave + lane;
+            if (idx < nch) v[q] = ld16(xrow + idx * 16);
+        }
+        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+            const int my = load_slot_block(tok_slot, jb, sp.j1);
+            const int n = min(kWave, sp.j1 - jb);
+            for (int u = 0; u < n; ++u) {
+                const int s = __builtin_amdgcn_readlane(my, u);
+                if (s < 0 || (int64_t)s >= cap) continue;
+                char* dst = xp + (int64_t)s * rb;
+#pragma unroll
+                for (int q = 0; q < PCH; ++q) {
+                    const int64_t idx = c0 + q * kWave + lane;
+                    if (idx < nch) st16(dst + idx * 16, v[q]);
+                }
+            }
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kRowThreads) void dispatch_fwd_elem(
+    const char* __restrict__ x, int T, int64_t d, const int32_t* __restrict__ tok_off,
+    const int32_t* __restrict__ tok_slot, int64_t cap, char* __restrict__ xp)
+{
+    TokenSpan sp;
+    if (!token_span(T, tok_off, cap, sp)) return;
+    const int lane = lane_id();
+    for (int j = sp.j0; j < sp.j1; ++j) {
+        const int s = tok_slot[j];
+        if (s < 0 || (int64_t)s >= cap) continue;
+        for (int64_t c = lane; c < d; c += kWave)
+            store_elem<DT>(xp, (int64_t)s * d + c, load_elem<DT>(x, (int64_t)sp.t * d + c));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine forward: Y[t] = sum_s gate[s] * Yp[s] (fma chain in ascending expert
+// order); with gate == nullptr this is the dispatch backward dX[t] = sum dXp[s]
+// ---------------------------------------------------------------------------
+
+template <int DT, int PCH>
+__global__ __launch_bounds__(kRowThreads) void combine_fwd_vec(
+    const char* __restrict__ yp, const float* __restrict__ gate, int T, int64_t nch,
+    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, int64_t cap,
+    char* __restrict__ y)
+{
+    using P = Pack<DT>;
+    constexpr int N = P::N;
+    TokenSpan sp;
+    if (!token_span(T, tok_off, cap, sp)) return;
+    const int lane = lane_id();
+    const int64_t rb = nch * 16;
+    for (int64_t c0 = 0; c0 < nch; c0 += PCH * kWave) {
+        float acc[PCH][N];
+#pragma unroll
+        for (int q = 0; q < PCH; ++q)
+#pragma unroll
+            for (int i = 0; i < N; ++i) acc[q][i] = 0.0f;
+        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+            const int my = load_slot_block(tok_slot, jb, sp.j1);
+            const int n = min(kWave, sp.j1 - jb);
+            for (int u = 0; u < n; ++u) {
+                const int s = __builtin_amdgcn_readlane(my, u);
+                if (s < 0 || (int64_t)s >= cap) continue;
+                const float g = gate ? gate[s] : 1.0f;
+                const char* src = yp + (int64_t)s * rb;
+                v4u w[PCH];
+#pragma unroll
+                for (int q = 0; q < PCH; ++q) {
+                    const int64_t idx = c0 + q * kWave + lane;
+                    if (idx < nch) w[q] = ld16(src + idx * 16);
+                }
+#pragma unroll
+                for (int q = 0; q < PCH; ++q) {
+                    const int64_t idx = c0 + q * kWave + lane;
+                    if (idx < nch) {
+                        float f[N];
+                        P::unpack(w[q], f);
+#pragma unroll
+                        for (int i = 0; i < N; ++i) acc[q][i] = __builtin_fmaf(g, f[i], acc[q][i]);
+                    }
+                }
+            }
+        }
+        char* dst = y + (int64_t)sp.t * rb;
+#pragma unroll
+        for (int q = 0; q < PCH; ++q) {
+            const int64_t idx = c0 + q * kWave + lane;
+            if (idx < nch) st16(dst + idx * 16, P::pack(acc[q]));
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kRowThreads) void combine_fwd_elem(
+    const char* __restrict__ yp, const float* __restrict__ gate, int T, int64_t d,
+    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, int64_t cap,
+    char* __restrict__ y)
+{
+    TokenSpan sp;
+    if (!token_span(T, tok_off, cap, sp)) return;
+    const int lane = lane_id();
+    for (int64_t c = lane; c < d; c += kWave) {
+        float acc = 0.0f;
+        for (int j = sp.j0; j < sp.j1; ++j) {
+            const int s = tok_slot[j];
+            if (s < 0 || (int64_t)s >= cap) continue;
+            const float g = gate ? gate[s] : 1.0f;
+            acc = __builtin_fmaf(g, load_elem<DT>(yp, (int64_t)s * d + c), acc);
+        }
+        store_elem<DT>(y, (int64_t)sp.t * d + c, acc);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine backward: dYp[s] = gate[s] * dY[t]; dgate[s] = <dY[t], Yp[s]>;
+// dlogits[t, e(s)] = dgate[s] * g (1 - g), zero for unselected experts.
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxLanesE = ET_MAX_EXPERTS / kWave;  // expert registers per lane
+
+// Expert of slot s: the largest e with eoff[e] <= s (binary search in LDS).
+__device__ __forceinline__ int expert_of_slot(const int* eoff_lds, int E, int s)
+{
+    int lo = 0, hi = E;  // eoff[lo] <= s < eoff[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (eoff_lds[mid] <= s) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+// Records slot s's results: dgate, and the dlogits value in the lane/register
+// that owns expert e(s) of this token's dlogits row.
+__device__ __forceinline__ void finish_slot(int s, float dot, float g, float* __restrict__ dgate,
+                                            const int* eoff_lds, int E, bool want_dl, float* dlv)
+{
+    if (lane_id() == 0) dgate[s] = dot;
+    if (want_dl) {
+        const int e = expert_of_slot(eoff_lds, E, s);
+        const float v = dot * (g * (1.0f - g));
+        const int reg = e >> 6;
+        const bool mine = (e & (kWave - 1)) == lane_id();
+#pragma unroll
+        for (int i = 0; i < kMaxLanesE; ++i)
+            if (i == reg && mine) dlv[i] = v;
+    }
+}
+
+__device__ __forceinline__ void write_dlogits_row(float* __restrict__ dlogits, int t, int E, const float* dlv)
+{
+    float* row = dlogits + (int64_t)t * E;
+#pragma unroll
+    for (int i = 0; i < kMaxLanesE; ++i) {
+        const int e = i * kWave + lane_id();
+        if (e < E) row[e] = dlv[i];
+    }
+}
+
+__device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __restrict__ eoff, int E,
+                                              bool want_dl)
+{
+    if (want_dl)
+        for (int e = threadIdx.x; e <= E; e += kRowThreads) eoff_lds[e] = eoff[e];
+    __syncthreads();
+}
+
+template <int DT, int PCH>
+__global__ __launch_bounds__(kRowThreads) void combine_bwd_vec(
+    const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate,
+    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot,
+    const int32_t* __restrict__ eoff, int T, int E, int64_t nch, int64_t cap,
+    char* __restrict__ dyp, float* __restrict__ dgate, float* __restrict__ dlogits)
+{
+    using P = Pack<DT>;
+    constexpr int N = P::N;
+    __shared__ int eoff_lds[ET_MAX_EXPERTS + 1];
+    __shared__ float dotbuf[kRowWaves][ET_MAX_EXPERTS];
+    const bool want_dl = dlogits != nullptr;
+    load_eoff_lds(eoff_lds, eoff, E, want_dl);
+    TokenSpan sp;
+    if (!token_span(T, tok_off, cap, sp)) return;
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int64_t rb = nch * 16;
+    const bool multi = nch > (int64_t)PCH * kWave;
+    float dlv[kMaxLanesE];
+#pragma unroll
+    for (int i = 0; i < kMaxLanesE; ++i) dlv[i] = 0.0f;
+
+    const char* dyrow = dy + (int64_t)sp.t * rb;
+    for (int64_t c0 = 0; c0 < nch; c0 += PCH * kWave) {
+        float df[PCH][N];
+#pragma unroll
+        for (int q = 0; q < PCH; ++q) {
+            const int64_t idx = c0 + q * kWave + lane;
+            if (idx < nch) P::unpack(ld16(dyrow + idx * 16), df[q]);
+            else
+#pragma unroll
+                for (int i = 0; i < N; ++i) df[q][i] = 0.0f;
+        }
+        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+            const int my = load_slot_block(tok_slot, jb, sp.j1);
+            const int n = min(kWave, sp.j1 - jb);
+            for (int u = 0; u < n; ++u) {
+                const int s = __builtin_amdgcn_readlane(my, u);
+                if (s < 0 || (int64_t)s >= cap) continue;
+                const float g = gate[s];
+                const char* src = yp + (int64_t)s * rb;
+                char* dst = dyp + (int64_t)s * rb;
+                v4u w[PCH];
+#pragma unroll
+                for (int q = 0; q < PCH; ++q) {
+                    const int64_t idx = c0 + q * kWave + lane;
+                    if (idx < nch) w[q] = ld16(src + idx * 16);
+                }
+                float part = 0.0f;
+#pragma unroll
+                for (int q = 0; q < PCH; ++q) {
+                    const int64_t idx = c0 + q * kWave + lane;
+                    if (idx < nch) {
+                        float f[N], o[N];
+                        P::unpack(w[q], f);
+#pragma unroll
+                        for (int i = 0; i < N; ++i) {
+                            part = __builtin_fmaf(df[q][i], f[i], part);
+                            o[i] = g * df[q][i];
+                        }
+                        st16(dst + idx * 16, P::pack(o));
+                    }
+                }
+                const float dot = wave_sum(part);
+                if (!multi) {
+                    finish_slot(s, dot, g, dgate, eoff_lds, E, want_dl, dlv);
+                } else if (lane == 0 && jb + u - sp.j0 < ET_MAX_EXPERTS) {
+                    float* slotp = &dotbuf[wave][jb + u - sp.j0];
+                    *slotp = (c0 == 0) ? dot : *slotp + dot;
+                }
+            }
+        }
+    }
+    if (multi) {
+        // lane 0 alone wrote dotbuf; it reads back and broadcasts
+        for (int j = sp.j0; j < sp.j1; ++j) {
+            const int s = tok_slot[j];
+            if (s < 0 || (int64_t)s >= cap) continue;
+            const float mine = (lane == 0 && j - sp.j0 < ET_MAX_EXPERTS) ? dotbuf[wave][j - sp.j0] : 0.0f;
+            const float dot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mine)));
+            finish_slot(s, dot, gate[s], dgate, eoff_lds, E, want_dl, dlv);
+        }
+    }
+    if (want_dl) write_dlogits_row(dlogits, sp.t, E, dlv);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kRowThreads) void combine_bwd_elem(
+    const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate,
+    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot,
+    const int32_t* __restrict__ eoff, int T, int E, int64_t d, int64_t cap,
+    char* __restrict__ dyp, float* __restrict__ dgate, float* __restrict__ dlogits)
+{
+    __shared__ int eoff_lds[ET_MAX_EXPERTS + 1];
+    const bool want_dl = dlogits != nullptr;
+    load_eoff_lds(eoff_lds, eoff, E, want_dl);
+    TokenSpan sp;
+    if (!token_span(T, tok_off, cap, sp)) return;
+    const int lane = lane_id();
+    float dlv[kMaxLanesE];
+#pragma unroll
+    for (int i = 0; i < kMaxLanesE; ++i) dlv[i] = 0.0f;
+    for (int j = sp.j0; j < sp.j1; ++j) {
+        const int s = tok_slot[j];
+        if (s < 0 || (int64_t)s >= cap) continue;
+        const float g = gate[s];
+        float part = 0.0f;
+        for (int64_t c = lane; c < d; c += kWave) {
+            const float dv = load_elem<DT>(dy, (int64_t)sp.t * d + c);
+            part = __builtin_fmaf(dv, load_elem<DT>(yp, (int64_t)s * d + c), part);
+            store_elem<DT>(dyp, (int64_t)s * d + c, g * dv);
+        }
+        finish_slot(s, wave_sum(part), g, dgate, eoff_lds, E, want_dl, dlv);
+    }
+    if (want_dl) write_dlogits_row(dlogits, sp.t, E, dlv);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int elem_bytes(int dtype) { return dtype == ET_DTYPE_BF16 ? 2 : 4; }
+
+static int check_common(const char* fn, int64_t T, int64_t d, int dtype, int64_t cap,
+                        const int32_t* tok_off, const int32_t* tok_slot)
+{
+    if (T < 0 || T >= (int64_t(1) << 31)) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": num_tokens out of range");
+    if (d < 0) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": d < 0");
+    if (dtype != ET_DTYPE_F32 && dtype != ET_DTYPE_BF16)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": dtype must be ET_DTYPE_F32 or ET_DTYPE_BF16");
+    if (cap < 0) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": slot_capacity < 0");
+    if (T > 0 && (!tok_off || (cap > 0 && !tok_slot)))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null token_offsets/token_slot");
+    return ET_OK;
+}
+
+// Passes of PCH 16-byte chunks per lane: the smallest PCH in {1,2,4,8} that
+// covers the row in one pass, else 8 (multi-pass).
+static int pick_pch(int64_t nch)
+{
+    if (nch <= 1 * kWave) return 1;
+    if (nch <= 2 * kWave) return 2;
+    if (nch <= 4 * kWave) return 4;
+    return 8;
+}
+
+#define ET_SWITCH_PCH(pch, ...)                      \
+    switch (pch) {                                   \
+        case 1: { constexpr int PCH = 1; __VA_ARGS__; } break; \
+        case 2: { constexpr int PCH = 2; __VA_ARGS__; } break; \
+        case 4: { constexpr int PCH = 4; __VA_ARGS__; } break; \
+        default: { constexpr int PCH = 8; __VA_ARGS__; } break; \
+    }
+
+#define ET_SWITCH_DT(dt, ...)                                          \
+    if ((dt) == ET_DTYPE_BF16) { constexpr int DT = ET_DTYPE_BF16; __VA_ARGS__; } \
+    else { constexpr int DT = ET_DTYPE_F32; __VA_ARGS__; }
+
+static dim3 row_grid(int64_t T) { return dim3((unsigned)((T + kRowWaves - 1) / kRowWaves)); }
+
+}  // namespace et
+
+using namespace et;
+
+extern "C" int et_dispatch_fwd(const void* x, int64_t T, int64_t d, int dtype,
+                               const int32_t* token_offsets, const int32_t* token_slot,
+                               int64_t cap, void* xp, void* stream)
+{
+    if (int rc = check_common("et_dispatch_fwd", T, d, dtype, cap, token_offsets, token_slot)) return rc;
+    if (T == 0 || d == 0 || cap == 0) return ET_OK;
+    if (!x || !xp) return fail(ET_ERR_INVALID_ARGUMENT, "et_dispatch_fwd: null x/xp");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t rb = d * elem_bytes(dtype);
+    const char* xc = static_cast<const char*>(x);
+    char* xpc = static_cast<char*>(xp);
+    if (rb % 16 == 0 && aligned16(x) && aligned16(xp)) {
+        const int64_t nch = rb / 16;
+        ET_SWITCH_PCH(pick_pch(nch),
+                      dispatch_fwd_vec<PCH><<<row_grid(T), dim3(kRowThreads), 0, s>>>(xc, (int)T, nch, token_offsets, token_slot, cap, xpc));
+    } else {
+        ET_SWITCH_DT(dtype, dispatch_fwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(xc, (int)T, d, token_offsets, token_slot, cap, xpc));
+    }
+    return check_launch("dispatch_fwd");
+}
+
+static int combine_like(const char* fn, const void* yp, const float* gate, const int32_t* token_offsets,
+                        const int32_t* token_slot, int64_t T, int64_t d, int dtype, int64_t cap, void* y,
+                        void* stream)
+{
+    if (int rc = check_common(fn, T, d, dtype, cap, token_offsets, token_slot)) return rc;
+    if (T == 0 || d == 0) return ET_OK;
+    if (!y || (cap > 0 && !yp)) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null input/output");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t rb = d * elem_bytes(dtype);
+    const char* ypc = static_cast<const char*>(yp);
+    char* yc = static_cast<char*>(y);
+    if (rb % 16 == 0 && aligned16(yp) && aligned16(y)) {
+        const int64_t nch = rb / 16;
+        ET_SWITCH_DT(dtype, ET_SWITCH_PCH(pick_pch(nch),
+            combine_fwd_vec<DT, PCH><<<row_grid(T), dim3(kRowThreads), 0, s>>>(ypc, gate, (int)T, nch, token_offsets, token_slot, cap, yc)));
+    } else {
+        ET_SWITCH_DT(dtype, combine_fwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(ypc, gate, (int)T, d, token_offsets, token_slot, cap, yc));
+    }
+    return check_launch(fn);
+}
+
+extern "C" int et_combine_fwd(const void* yp, const float* slot_gate, const int32_t* token_offsets,
+                              const int32_t* token_slot, int64_t T, int64_t d, int dtype, int64_t cap,
+                              void* y, void* stream)
+{
+    if (cap > 0 && T > 0 && !slot_gate) return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_fwd: null slot_gate");
+    return combine_like("et_combine_fwd", yp, slot_gate, token_offsets, token_slot, T, d, dtype, cap, y, stream);
+}
+
+extern "C" int et_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
+                               int64_t T, int64_t d, int dtype, int64_t cap, void* dx, void* stream)
+{
+    return combine_like("et_dispatch_bwd", dxp, nullptr, token_offsets, token_slot, T, d, dtype, cap, dx, stream);
+}
+
+extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
+                              const int32_t* token_offsets, const int32_t* token_slot,
+                              const int32_t* expert_offsets, int64_t T, int64_t E, int64_t d, int dtype,
+                              int64_t cap, void* dyp, float* dgate, float* dlogits, void* stream)
+{
+    if (int rc = check_common("et_combine_bwd", T, d, dtype, cap, token_offsets, token_slot)) return rc;
+    if (E < 1 || E > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_EXPERTS) + "]");
+    if (dlogits && !expert_offsets)
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: dlogits needs expert_offsets");
+    if (T == 0) return ET_OK;
+    if (cap > 0 && (!slot_gate || !dgate || (d > 0 && (!dy || !yp || !dyp))))
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: null input/output");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t rb = d * elem_bytes(dtype);
+    const char* dyc = static_cast<const char*>(dy);
+    const char* ypc = static_cast<const char*>(yp);
+    char* dypc = static_cast<char*>(dyp);
+    if (d > 0 && rb % 16 == 0 && aligned16(dy) && aligned16(yp) && aligned16(dyp)) {
+        const int64_t nch = rb / 16;
+        ET_SWITCH_DT(dtype, ET_SWITCH_PCH(pick_pch(nch),
+            combine_bwd_vec<DT, PCH><<<row_grid(T), dim3(kRowThreads), 0, s>>>(dyc, ypc, slot_gate, token_offsets, token_slot, expert_offsets, (int)T, (int)E, nch, cap, dypc, dgate, dlogits)));
+    } else {
+        ET_SWITCH_DT(dtype, combine_bwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(dyc, ypc, slot_gate, token_offsets, token_slot, expert_offsets, (int)T, (int)E, d, cap, dypc, dgate, dlogits));
+    }
+    return check_launch("et_combine_bwd");
+}

@@ -1,0 +1,378 @@
+"""Host-side API of the Expert-Threshold MoE token-dispatch path.
+
+Every function validates its arguments in Python (raising ValueError or
+TypeError before anything reaches the device), allocates outputs with torch's
+caching allocator, and calls one entry point of libetmoe.so on torch's current
+HIP stream.  torch is only plumbing here -- device memory and streams; all
+arithmetic runs in the HIP kernels.  There is no CPU fallback: without the
+library every call raises.
+
+The reference tree (bat0001/peer-review-agents) has no operator for this path
+(it is an agent-launcher CLI; its only plug-in points are the backend registry
+at cli/reva/backends.py:28-131 and the translator table at
+cli/reva/translators/__init__.py:33-53), so the names and signatures below are
+this package's own.
+
+Data layout after routing (all int32 except slot_gate):
+    counts[E], expert_offsets[E+1]      CSR of slots by expert
+    token_offsets[T+1], token_slot[S]   CSR of slots by token (ascending expert)
+    sorted_token[S], slot_gate[S]       slot -> token id, slot -> gate (score)
+Slots are ordered by (expert, token id).  Slot-major activations (Xp, Yp, dYp,
+dXp) have one row per slot.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from ._lib import ET_DTYPE_BF16, ET_DTYPE_F32, ET_MAX_EXPERTS, check, lib
+
+_ACT_DTYPES = {torch.float32: ET_DTYPE_F32, torch.bfloat16: ET_DTYPE_BF16}
+
+
+# --------------------------------------------------------------------------- #
+# helpers
+# --------------------------------------------------------------------------- #
+
+def _vp(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_device(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a HIP device, got {t.device}")
+
+
+def _require(t: torch.Tensor, name: str, dtype, ndim: int, device=None) -> None:
+    _require_device(t, name)
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _act_dtype(t: torch.Tensor, name: str) -> int:
+    if t.dtype not in _ACT_DTYPES:
+        raise TypeError(f"{name} must be float32 or bfloat16, got {t.dtype}")
+    return _ACT_DTYPES[t.dtype]
+
+
+def _require_act(t: torch.Tensor, name: str, device=None) -> int:
+    _require_device(t, name)
+    dt = _act_dtype(t, name)
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D [rows, d], got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    return dt
+
+
+# --------------------------------------------------------------------------- #
+# routing
+# --------------------------------------------------------------------------- #
+
+@dataclass
+class RoutingPlan:
+    """Result of :func:`route`.
+
+    ``num_slots`` is the host-side slot count S when routing synchronised to
+    read it (the default); the slot arrays are then exactly S long.  With an
+    explicit ``slot_capacity`` routing does not synchronise, ``num_slots`` is
+    None and the slot arrays have ``capacity`` entries of which the first
+    ``expert_offsets[E]`` are valid.
+    """
+
+    counts: torch.Tensor
+    expert_offsets: torch.Tensor
+    token_offsets: torch.Tensor
+    sorted_token: torch.Tensor
+    slot_gate: torch.Tensor
+    token_slot: torch.Tensor
+    num_tokens: int
+    num_experts: int
+    capacity: int
+    num_slots: Optional[int] = None
+
+    @property
+    def rows(self) -> int:
+        """Rows of a slot-major activation buffer for this plan."""
+        return self.num_slots if self.num_slots is not None else self.capacity
+
+    @property
+    def device(self) -> torch.device:
+        return self.expert_offsets.device
+
+
+def route_workspace_bytes(num_tokens: int, num_experts: int) -> int:
+    return int(lib().et_route_workspace_bytes(num_tokens, num_experts))
+
+
+def route(logits: torch.Tensor, thr: torch.Tensor, *, slot_capacity: Optional[int] = None,
+          workspace: Optional[torch.Tensor] = None) -> RoutingPlan:
+    """Threshold routing + CSR + stable permutation indices.
+
+    logits: float32 [T, E] router logits (score = sigmoid(logit)).
+    thr:    float32 [E] per-expert thresholds.
+    (t, e) is routed iff score >= thr[e]; a token with no expert goes to its
+    argmax expert.  Deterministic: identical inputs give identical bits.
+    """
+    _require(logits, "logits", torch.float32, 2)
+    dev = logits.device
+    T, E = logits.shape
+    _require(thr, "thr", torch.float32, 1, dev)
+    if thr.shape[0] != E:
+        raise ValueError(f"thr has {thr.shape[0]} entries, logits has {E} experts")
+    if not 1 <= E <= ET_MAX_EXPERTS:
+        raise ValueError(f"num_experts must be in [1, {ET_MAX_EXPERTS}], got {E}")
+    if T * E >= 2 ** 31:
+        raise ValueError("num_tokens * num_experts must be < 2^31 (int32 slot indices)")
+    sync = slot_capacity is None
+    cap = T * E if sync else int(slot_capacity)
+    if cap < 0:
+        raise ValueError("slot_capacity must be >= 0")
+    i32 = dict(dtype=torch.int32, device=dev)
+    counts = torch.empty(E, **i32)
+    eo = torch.empty(E + 1, **i32)
+    to = torch.empty(T + 1, **i32)
+    st = torch.empty(cap, **i32)
+    sg = torch.empty(cap, dtype=torch.float32, device=dev)
+    ts = torch.empty(cap, **i32)
+    wsb = route_workspace_bytes(T, E)
+    if workspace is None:
+        workspace = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace must hold {wsb} bytes on {dev}")
+    with torch.cuda.device(dev):
+        rc = lib().et_route(_vp(logits), _vp(thr), T, E, _vp(counts), _vp(eo), _vp(to), _vp(st),
+                            _vp(sg), _vp(ts), cap, _vp(workspace), wsb, _stream(dev))
+    check("et_route", rc)
+    plan = RoutingPlan(counts, eo, to, st, sg, ts, T, E, cap)
+    if sync:
+        S = int(eo[E].item())
+        plan.num_slots = S
+        plan.sorted_token = st[:S]
+        plan.slot_gate = sg[:S]
+        plan.token_slot = ts[:S]
+        plan.capacity = S
+    return plan
+
+
+# --------------------------------------------------------------------------- #
+# dispatch / combine
+# --------------------------------------------------------------------------- #
+
+def _out_or_new(out, shape, dtype, dev, name):
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=dev)
+    _require(out, name, dtype, len(shape), dev)
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(out.shape)}")
+    return out
+
+
+def _check_plan(plan: RoutingPlan, dev: torch.device) -> None:
+    if plan.device != dev:
+        raise ValueError(f"plan is on {plan.device}, tensors are on {dev}")
+
+
+def dispatch(x: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Permute (scatter): Xp[slot] = X[token(slot)].  x: [T, d] f32/bf16."""
+    dt = _require_act(x, "x")
+    dev = x.device
+    _check_plan(plan, dev)
+    T, d = x.shape
+    if T != plan.num_tokens:
+        raise ValueError(f"x has {T} tokens, plan has {plan.num_tokens}")
+    xp = _out_or_new(out, (plan.rows, d), x.dtype, dev, "out")
+    with torch.cuda.device(dev):
+        rc = lib().et_dispatch_fwd(_vp(x), T, d, dt, _vp(plan.token_offsets), _vp(plan.token_slot),
+                                   plan.rows, _vp(xp), _stream(dev))
+    check("et_dispatch_fwd", rc)
+    return xp
+
+
+def combine(yp: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Un-permute with gate-weighted combine: Y[t] = sum_s gate[s] * Yp[s]."""
+    dt = _require_act(yp, "yp")
+    dev = yp.device
+    _check_plan(plan, dev)
+    if yp.shape[0] != plan.rows:
+        raise ValueError(f"yp has {yp.shape[0]} rows, plan has {plan.rows} slots")
+    T, d = plan.num_tokens, yp.shape[1]
+    y = _out_or_new(out, (T, d), yp.dtype, dev, "out")
+    with torch.cuda.device(dev):
+        rc = lib().et_combine_fwd(_vp(yp), _vp(plan.slot_gate), _vp(plan.token_offsets),
+                                  _vp(plan.token_slot), T, d, dt, plan.rows, _vp(y), _stream(dev))
+    check("et_combine_fwd", rc)
+    return y
+
+
+def combine_backward(dy: torch.Tensor, yp: torch.Tensor, plan: RoutingPlan, *,
+                     need_dlogits: bool = False, out_dyp: Optional[torch.Tensor] = None,
+                     out_dgate: Optional[torch.Tensor] = None,
+                     out_dlogits: Optional[torch.Tensor] = None):
+    """Fused backward of combine.
+
+    Returns (dYp [S, d], dgate f32 [S], dlogits f32 [T, E] or None) with
+    dYp[s] = gate[s] * dY[t], dgate[s] = <dY[t], Yp[s]>,
+    dlogits[t, e] = dgate[s] * gate[s] * (1 - gate[s]) (0 where not routed).
+    """
+    dt = _require_act(dy, "dy")
+    dev = dy.device
+    if _require_act(yp, "yp", dev) != dt:
+        raise TypeError("dy and yp must have the same dtype")
+    _check_plan(plan, dev)
+    T, d = dy.shape
+    if T != plan.num_tokens:
+        raise ValueError(f"dy has {T} tokens, plan has {plan.num_tokens}")
+    if tuple(yp.shape) != (plan.rows, d):
+        raise ValueError(f"yp must have shape {(plan.rows, d)}, got {tuple(yp.shape)}")
+    E = plan.num_experts
+    dyp = _out_or_new(out_dyp, (plan.rows, d), dy.dtype, dev, "out_dyp")
+    dgate = _out_or_new(out_dgate, (plan.rows,), torch.float32, dev, "out_dgate")
+    dl = None
+    if need_dlogits or out_dlogits is not None:
+        dl = _out_or_new(out_dlogits, (T, E), torch.float32, dev, "out_dlogits")
+    with torch.cuda.device(dev):
+        rc = lib().et_combine_bwd(_vp(dy), _vp(yp), _vp(plan.slot_gate), _vp(plan.token_offsets),
+                                  _vp(plan.token_slot), _vp(plan.expert_offsets), T, E, d, dt,
+                                  plan.rows, _vp(dyp), _vp(dgate), _vp(dl), _stream(dev))
+    check("et_combine_bwd", rc)
+    return dyp, dgate, dl
+
+
+def dispatch_backward(dxp: torch.Tensor, plan: RoutingPlan,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Backward of dispatch: dX[t] = sum of dXp over t's slots (ascending expert)."""
+    dt = _require_act(dxp, "dxp")
+    dev = dxp.device
+    _check_plan(plan, dev)
+    if dxp.shape[0] != plan.rows:
+        raise ValueError(f"dxp has {dxp.shape[0]} rows, plan has {plan.rows} slots")
+    T, d = plan.num_tokens, dxp.shape[1]
+    dx = _out_or_new(out, (T, d), dxp.dtype, dev, "out")
+    with torch.cuda.device(dev):
+        rc = lib().et_dispatch_bwd(_vp(dxp), _vp(plan.token_offsets), _vp(plan.token_slot), T, d, dt,
+                                   plan.rows, _vp(dx), _stream(dev))
+    check("et_dispatch_bwd", rc)
+    return dx
+
+
+# --------------------------------------------------------------------------- #
+# EMA threshold update
+# --------------------------------------------------------------------------- #
+
+def threshold_workspace_bytes(num_tokens: int, num_experts: int) -> int:
+    return int(lib().et_threshold_workspace_bytes(num_tokens, num_experts))
+
+
+def threshold_update_(thr: torch.Tensor, logits: torch.Tensor, k_target: int,
+                      momentum: float = 0.99, *, stat: Optional[torch.Tensor] = None,
+                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """In-place EMA update of thr from this batch; returns the statistic.
+
+    stat[e] = c-th largest score of expert e, c = ceil(T * k_target / E);
+    thr[e]  = fma(momentum, thr[e], (1 - momentum) * stat[e]).
+    """
+    _require(logits, "logits", torch.float32, 2)
+    dev = logits.device
+    T, E = logits.shape
+    _require(thr, "thr", torch.float32, 1, dev)
+    if thr.shape[0] != E:
+        raise ValueError(f"thr has {thr.shape[0]} entries, logits has {E} experts")
+    if not 1 <= E <= ET_MAX_EXPERTS:
+        raise ValueError(f"num_experts must be in [1, {ET_MAX_EXPERTS}], got {E}")
+    if not 1 <= int(k_target) <= E:
+        raise ValueError(f"k_target must be in [1, {E}], got {k_target}")
+    if not 0.0 <= float(momentum) <= 1.0:
+        raise ValueError(f"momentum must be in [0, 1], got {momentum}")
+    stat = _out_or_new(stat, (E,), torch.float32, dev, "stat")
+    wsb = threshold_workspace_bytes(T, E)
+    if workspace is None:
+        workspace = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace must hold {wsb} bytes on {dev}")
+    with torch.cuda.device(dev):
+        rc = lib().et_threshold_update(_vp(logits), _vp(thr), T, E, int(k_target), float(momentum),
+                                       _vp(stat), _vp(workspace), wsb, _stream(dev))
+    check("et_threshold_update", rc)
+    return stat
+
+
+# --------------------------------------------------------------------------- #
+# autograd wrappers
+# --------------------------------------------------------------------------- #
+
+class _DispatchFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, plan):
+        ctx.plan = plan
+        return dispatch(x, plan)
+
+    @staticmethod
+    def backward(ctx, dxp):
+        return dispatch_backward(dxp.contiguous(), ctx.plan), None
+
+
+class _CombineFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, yp, logits, plan):
+        ctx.plan = plan
+        ctx.save_for_backward(yp)
+        return combine(yp, plan)
+
+    @staticmethod
+    def backward(ctx, dy):
+        (yp,) = ctx.saved_tensors
+        dyp, _dgate, dl = combine_backward(dy.contiguous(), yp, ctx.plan,
+                                           need_dlogits=ctx.needs_input_grad[1])
+        return dyp, dl, None
+
+
+def dispatch_autograd(x: torch.Tensor, plan: RoutingPlan) -> torch.Tensor:
+    """dispatch() with a backward that runs dispatch_backward()."""
+    return _DispatchFn.apply(x, plan)
+
+
+def combine_autograd(yp: torch.Tensor, logits: torch.Tensor, plan: RoutingPlan) -> torch.Tensor:
+    """combine() differentiable in yp and in the router logits (through the
+    gates, which are sigmoid(logits) at the routed pairs; the routing mask
+    itself is piecewise constant and has no gradient)."""
+    return _CombineFn.apply(yp, logits, plan)
+
+
+class ExpertThresholdRouter(torch.nn.Module):
+    """Per-expert thresholds with the EMA update applied after each training
+    batch (route with the current thresholds, then update them from the batch),
+    the way batch statistics are kept in a running buffer."""
+
+    def __init__(self, num_experts: int, k_target: int, momentum: float = 0.99,
+                 init_threshold: float = 0.5, device=None):
+        super().__init__()
+        if not 1 <= k_target <= num_experts:
+            raise ValueError("k_target must be in [1, num_experts]")
+        self.k_target = int(k_target)
+        self.momentum = float(momentum)
+        self.register_buffer("thr", torch.full((num_experts,), float(init_threshold),
+                                               dtype=torch.float32, device=device))
+
+    def forward(self, logits: torch.Tensor, *, slot_capacity: Optional[int] = None) -> RoutingPlan:
+        plan = route(logits.detach(), self.thr, slot_capacity=slot_capacity)
+        if self.training:
+            threshold_update_(self.thr, logits.detach(), self.k_target, self.momentum)
+        return plan

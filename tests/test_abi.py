@@ -1,0 +1,98 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/etmoe.h, and rejects bad arguments before enqueueing any
+device work (these calls return before touching the HIP runtime)."""
+import ctypes
+import os
+
+import pytest
+
+from conftest import ROOT
+
+ET_ERR_INVALID_ARGUMENT = -1
+ET_ERR_WORKSPACE_TOO_SMALL = -2
+
+
+def test_library_exports_every_header_symbol(et):
+    syms = et.header_symbols()
+    assert len(syms) == 10
+    lib = et.lib()
+    for name in syms:
+        assert hasattr(lib, name), name
+    raw = ctypes.CDLL(et.LIB_PATH)                # plain dlopen/dlsym view as well
+    for name in syms:
+        assert getattr(raw, name) is not None
+
+
+def test_abi_version_and_header_agree(et):
+    hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
+    assert "#define ET_ABI_VERSION 1" in hdr
+    assert et.lib().et_abi_version() == 1
+
+
+def test_workspace_sizes(et):
+    lib = et.lib()
+    assert lib.et_route_workspace_bytes(65536, 128) >= 2 * 256 * 128 * 4
+    assert lib.et_route_workspace_bytes(0, 8) > 0
+    assert lib.et_route_workspace_bytes(10, 0) == 0
+    assert lib.et_threshold_workspace_bytes(131072, 64) >= 64 * 256 * 4
+    assert lib.et_threshold_workspace_bytes(10, 0) == 0
+
+
+def _err(et):
+    return et.lib().et_last_error().decode()
+
+
+def test_route_rejects_bad_arguments_without_launching(et):
+    lib = et.lib()
+    ws = ctypes.c_void_p(0x1000)
+    dummy = ctypes.c_void_p(0x2000)
+    rc = lib.et_route(dummy, dummy, 16, 0, dummy, dummy, dummy, dummy, dummy, dummy, 16, ws, 1 << 20, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT and "num_experts" in _err(et)
+    rc = lib.et_route(dummy, dummy, 16, 2000, dummy, dummy, dummy, dummy, dummy, dummy, 16, ws, 1 << 20, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT
+    rc = lib.et_route(dummy, dummy, 1 << 26, 64, dummy, dummy, dummy, dummy, dummy, dummy, 16, ws, 1 << 30, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT and "2^31" in _err(et)
+    rc = lib.et_route(None, dummy, 16, 4, dummy, dummy, dummy, dummy, dummy, dummy, 16, ws, 1 << 20, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT and "logits" in _err(et)
+    rc = lib.et_route(dummy, dummy, 16, 4, dummy, dummy, dummy, None, dummy, dummy, 16, ws, 1 << 20, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT
+    rc = lib.et_route(dummy, dummy, 4096, 8, dummy, dummy, dummy, dummy, dummy, dummy, 16, ws, 16, None)
+    assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "workspace" in _err(et)
+
+
+def test_row_entry_points_reject_bad_arguments(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    assert lib.et_dispatch_fwd(p, 8, 16, 7, p, p, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "dtype" in _err(et)
+    assert lib.et_dispatch_fwd(p, -1, 16, 0, p, p, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_dispatch_fwd(p, 8, 16, 0, None, p, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_combine_fwd(p, None, p, p, 8, 16, 1, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_dispatch_bwd(p, p, p, 8, -3, 1, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_combine_bwd(p, p, p, p, p, None, 8, 4, 16, 0, 8, p, p, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "expert_offsets" in _err(et)
+    assert lib.et_combine_bwd(p, p, p, p, p, p, 8, 0, 16, 0, 8, p, p, p, None) == ET_ERR_INVALID_ARGUMENT
+    # zero-size work is a successful no-op that launches nothing
+    assert lib.et_dispatch_fwd(p, 0, 16, 0, p, p, 8, p, None) == 0
+    assert lib.et_combine_fwd(p, p, p, p, 0, 16, 0, 8, p, None) == 0
+
+
+def test_threshold_update_rejects_bad_arguments(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    assert lib.et_threshold_update(p, p, 16, 8, 0, 0.99, None, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_threshold_update(p, p, 16, 8, 9, 0.99, None, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_threshold_update(p, p, 16, 8, 2, 1.5, None, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_threshold_update(p, p, 16, 8, 2, float("nan"), None, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_threshold_update(p, p, 16, 8, 2, 0.9, None, p, 8, None) == ET_ERR_WORKSPACE_TOO_SMALL
+    # an empty batch is a no-op
+    assert lib.et_threshold_update(p, p, 0, 8, 2, 0.9, None, p, 1 << 20, None) == 0
+
+
+def test_error_string_is_per_call(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    lib.et_dispatch_fwd(p, 8, 16, 9, p, p, 8, p, None)
+    first = _err(et)
+    lib.et_threshold_update(p, p, 16, 8, 0, 0.99, None, p, 1 << 20, None)
+    assert _err(et) != first and "k_target" in _err(et)
