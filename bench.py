@@ -65,6 +65,30 @@ def read_traffic(workload: str):
     return None
 
 
+def copy_ceiling(dev, stream, nbytes: int = 1 << 30, reps: int = 5) -> dict:
+    """Bandwidth of a plain streaming kernel on this GPU, measured in the same
+    run: torch's elementwise ``x * 1`` over ``nbytes`` of int32 in and ``nbytes``
+    out (each byte read once and written once), timed with events on ``stream``.
+    It is also the known-size kernel that calibrates the FETCH_SIZE and
+    WRITE_SIZE counters in a ``rocprofv3 --pmc`` run of this script."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    torch.mul(src, 1, out=dst)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        torch.mul(src, 1, out=dst)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del src, dst
+    return {"kernel": "torch elementwise x*1 (int32)", "bytes": 2 * nbytes, "ms": round(ms, 4),
+            "GB/s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(2 * nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
+
+
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
     """The CPU restatement (oracle/, single thread) on the first `tokens`
     tokens of the same workload, same ops as one GPU step."""
@@ -171,6 +195,7 @@ def main() -> int:
         if rc != 0:
             raise RuntimeError(f"stage {STAGES[i]} failed: {lib.et_last_error().decode()}")
 
+    copy_ref = copy_ceiling(dev, stream)
     for _ in range(args.warmup):
         for i in range(len(STAGES)):
             stage(i)
@@ -232,12 +257,16 @@ def main() -> int:
         "step_bytes": step_bytes,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "copy_ceiling": copy_ref,
         "kernels": kernels,
     }
     for name in STAGES:
         k = kernels[name]
         print(f"  {name:13s} {k['ms']:8.4f} ms  {k['GB/s']:8.1f} GB/s  {100 * k['frac']:5.1f}% of peak",
               file=sys.stderr)
+    print(f"  copy ref      {copy_ref['ms']:8.4f} ms  {copy_ref['GB/s']:8.1f} GB/s  "
+          f"{100 * copy_ref['frac']:5.1f}% of peak ({copy_ref['kernel']}, {copy_ref['bytes']} B)",
+          file=sys.stderr)
     print(f"  step {ms_per_step:.4f} ms, {slots_per_s / 1e6:.2f} M slots/s, "
           f"{100 * out['hbm_frac']:.1f}% of HBM peak", file=sys.stderr)
     print(json.dumps(out), flush=True)
