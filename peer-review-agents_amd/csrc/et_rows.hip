@@ -2,16 +2,20 @@
 // (permute), combine (gate-weighted un-permute), combine backward (dYp, dgate,
 // dlogits) and dispatch backward (dX).
 //
-// All four are token-major: one wave owns one token, reads its slot list
-// token_slot[token_offsets[t] .. token_offsets[t+1]) once, and moves whole
-// rows.  Token-major order is what makes the traffic minimal: X and dY rows
-// are read exactly once (then written or consumed k_t times from registers),
-// Y and dX rows are written exactly once, and sums over a token's slots are
-// formed in registers in ascending expert order without atomics.
+// All four are token-major: a token's slot list token_slot[token_offsets[t] ..
+// token_offsets[t+1]) is read by the waves that own the token, and whole rows
+// move.  Token-major order is what makes the traffic minimal: X and dY rows are
+// read exactly once (then written or consumed k_t times from registers), Y and
+// dX rows are written exactly once, and sums over a token's slots are formed in
+// registers in ascending expert order without atomics.
 //
-// Vector path: rows whose byte size is a multiple of 16 move as 16-byte
-// chunks, 64 lanes x 16 B = 1 KiB per wave instruction (fully coalesced), PCH
-// chunks per lane per pass over the row.  Other rows take the element path.
+// Vector path: rows whose byte size is a multiple of 16 move as 16-byte chunks,
+// 64 lanes x 16 B = 1 KiB per wave instruction (fully coalesced).  Dispatch and
+// combine split a row into pieces with one wave each; combine backward keeps a
+// whole row per wave so that each slot's dot product is one wave reduction.
+// Rows of other sizes take the element path.
+#include <algorithm>
+
 #include "et_common.hpp"
 
 namespace et {
@@ -102,39 +106,77 @@ __device__ __forceinline__ int load_slot_block(const int32_t* __restrict__ tok_s
 }
 
 // ---------------------------------------------------------------------------
-// dispatch forward: Xp[s] = X[t] for each slot s of t
+// Row pieces.  The vector dispatch and combine kernels split every row into
+// pieces of whole 16-byte chunks and give each (token, piece) pair its own
+// wave: consecutive waves take consecutive pieces of one token, then move to
+// the next token.  On gfx950 many short-lived waves that each move 1-4 KiB
+// stream closer to HBM peak than one wave looping over a whole row (measured
+// at d = 4096 bf16: 1 KiB pieces in 128-thread blocks for the scatter, 4 KiB
+// pieces with non-temporal loads and stores for the gathers).
 // ---------------------------------------------------------------------------
 
-template <int PCH>
-__global__ __launch_bounds__(kRowThreads) void dispatch_fwd_vec(
-    const char* __restrict__ x, int T, int64_t nch, const int32_t* __restrict__ tok_off,
-    const int32_t* __restrict__ tok_slot, int64_t cap, char* __restrict__ xp)
+struct PieceSpan {
+    int t;       // token
+    int64_t cb;  // first chunk of the wave's piece
+    int j0, j1;  // the token's slot-list entries, clamped to the capacity
+};
+
+// Wave -> (token, piece), for WPB waves per block and launches that cover
+// tokens [t_base, t_end).  False for the waves past t_end.
+template <int WPB>
+__device__ __forceinline__ bool piece_span(int t_base, int t_end, uint32_t npieces, int64_t piece_chunks,
+                                           const int32_t* __restrict__ tok_off, int64_t cap, PieceSpan& sp)
 {
-    TokenSpan sp;
-    if (!token_span(T, tok_off, cap, sp)) return;
-    const int lane = lane_id();
+    const uint32_t gw = blockIdx.x * (uint32_t)WPB +
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const uint32_t tl = gw / npieces;
+    const int64_t t = (int64_t)t_base + tl;
+    if (t >= t_end) return false;
+    sp.t = (int)t;
+    sp.cb = (int64_t)(gw - tl * npieces) * piece_chunks;
+    const int64_t a = tok_off[t];
+    const int64_t b = tok_off[t + 1];
+    sp.j0 = (int)min(a, cap);
+    sp.j1 = (int)max(min(b, cap), (int64_t)sp.j0);
+    return true;
+}
+
+__device__ __forceinline__ v4u ld16_nt(const char* p)
+{
+    return __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+}
+__device__ __forceinline__ void st16_nt(char* p, v4u v)
+{
+    __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(p));
+}
+
+// ---------------------------------------------------------------------------
+// dispatch forward: Xp[s] = X[t] for each slot s of t.  One wave per 1 KiB
+// piece of a token's row: each lane loads its 16-byte chunk once and stores it
+// to every slot of the token.
+// ---------------------------------------------------------------------------
+
+constexpr int kScatterWaves = 2;
+
+__global__ __launch_bounds__(kScatterWaves * kWave) void dispatch_fwd_vec(
+    const char* __restrict__ x, int t_base, int t_end, int64_t nch, uint32_t npieces,
+    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, int64_t cap,
+    char* __restrict__ xp)
+{
+    PieceSpan sp;
+    if (!piece_span<kScatterWaves>(t_base, t_end, npieces, kWave, tok_off, cap, sp)) return;
+    const int64_t idx = sp.cb + lane_id();
+    const bool on = idx < nch;
     const int64_t rb = nch * 16;
-    const char* xrow = x + (int64_t)sp.t * rb;
-    for (int64_t c0 = 0; c0 < nch; c0 += PCH * kWave) {
-        v4u v[PCH];
-#pragma unroll
-        for (int q = 0; q < PCH; ++q) {
-            const int64_t idx = c0 + q * kWave + lane;
-            if (idx < nch) v[q] = ld16(xrow + idx * 16);
-        }
-        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
-            const int my = load_slot_block(tok_slot, jb, sp.j1);
-            const int n = min(kWave, sp.j1 - jb);
-            for (int u = 0; u < n; ++u) {
-                const int s = __builtin_amdgcn_readlane(my, u);
-                if (s < 0 || (int64_t)s >= cap) continue;
-                char* dst = xp + (int64_t)s * rb;
-#pragma unroll
-                for (int q = 0; q < PCH; ++q) {
-                    const int64_t idx = c0 + q * kWave + lane;
-                    if (idx < nch) st16(dst + idx * 16, v[q]);
-                }
-            }
+    v4u v = {0u, 0u, 0u, 0u};
+    if (on) v = ld16(x + (int64_t)sp.t * rb + idx * 16);
+    for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+        const int my = load_slot_block(tok_slot, jb, sp.j1);
+        const int n = min(kWave, sp.j1 - jb);
+        for (int u = 0; u < n; ++u) {
+            const int s = __builtin_amdgcn_readlane(my, u);
+            if (s < 0 || (int64_t)s >= cap) continue;
+            if (on) st16(xp + (int64_t)s * rb + idx * 16, v);
         }
     }
 }
@@ -157,59 +199,61 @@ __global__ __launch_bounds__(kRowThreads) void dispatch_fwd_elem(
 
 // ---------------------------------------------------------------------------
 // combine forward: Y[t] = sum_s gate[s] * Yp[s] (fma chain in ascending expert
-// order); with gate == nullptr this is the dispatch backward dX[t] = sum dXp[s]
+// order).  Without GATE this is the dispatch backward dX[t] = sum dXp[s].  One
+// wave per piece of PCH * 64 chunks; the gathered rows are read once and never
+// again, so loads and the final store are non-temporal.
 // ---------------------------------------------------------------------------
 
-template <int DT, int PCH>
-__global__ __launch_bounds__(kRowThreads) void combine_fwd_vec(
-    const char* __restrict__ yp, const float* __restrict__ gate, int T, int64_t nch,
-    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, int64_t cap,
-    char* __restrict__ y)
+constexpr int kGatherWaves = 4;
+
+template <int DT, int PCH, bool GATE>
+__global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
+    const char* __restrict__ yp, const float* __restrict__ gate, int t_base, int t_end, int64_t nch,
+    uint32_t npieces, const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot,
+    int64_t cap, char* __restrict__ y)
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
-    TokenSpan sp;
-    if (!token_span(T, tok_off, cap, sp)) return;
+    PieceSpan sp;
+    if (!piece_span<kGatherWaves>(t_base, t_end, npieces, PCH * kWave, tok_off, cap, sp)) return;
     const int lane = lane_id();
     const int64_t rb = nch * 16;
-    for (int64_t c0 = 0; c0 < nch; c0 += PCH * kWave) {
-        float acc[PCH][N];
+    float acc[PCH][N];
 #pragma unroll
-        for (int q = 0; q < PCH; ++q)
+    for (int q = 0; q < PCH; ++q)
 #pragma unroll
-            for (int i = 0; i < N; ++i) acc[q][i] = 0.0f;
-        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
-            const int my = load_slot_block(tok_slot, jb, sp.j1);
-            const int n = min(kWave, sp.j1 - jb);
-            for (int u = 0; u < n; ++u) {
-                const int s = __builtin_amdgcn_readlane(my, u);
-                if (s < 0 || (int64_t)s >= cap) continue;
-                const float g = gate ? gate[s] : 1.0f;
-                const char* src = yp + (int64_t)s * rb;
-                v4u w[PCH];
+        for (int i = 0; i < N; ++i) acc[q][i] = 0.0f;
+    for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+        const int my = load_slot_block(tok_slot, jb, sp.j1);
+        const int n = min(kWave, sp.j1 - jb);
+        for (int u = 0; u < n; ++u) {
+            const int s = __builtin_amdgcn_readlane(my, u);
+            if (s < 0 || (int64_t)s >= cap) continue;
+            const float g = GATE ? gate[s] : 1.0f;
+            const char* src = yp + (int64_t)s * rb;
+            v4u w[PCH];
 #pragma unroll
-                for (int q = 0; q < PCH; ++q) {
-                    const int64_t idx = c0 + q * kWave + lane;
-                    if (idx < nch) w[q] = ld16(src + idx * 16);
-                }
+            for (int q = 0; q < PCH; ++q) {
+                const int64_t idx = sp.cb + q * kWave + lane;
+                if (idx < nch) w[q] = ld16_nt(src + idx * 16);
+            }
 #pragma unroll
-                for (int q = 0; q < PCH; ++q) {
-                    const int64_t idx = c0 + q * kWave + lane;
-                    if (idx < nch) {
-                        float f[N];
-                        P::unpack(w[q], f);
+            for (int q = 0; q < PCH; ++q) {
+                const int64_t idx = sp.cb + q * kWave + lane;
+                if (idx < nch) {
+                    float f[N];
+                    P::unpack(w[q], f);
 #pragma unroll
-                        for (int i = 0; i < N; ++i) acc[q][i] = __builtin_fmaf(g, f[i], acc[q][i]);
-                    }
+                    for (int i = 0; i < N; ++i) acc[q][i] = __builtin_fmaf(g, f[i], acc[q][i]);
                 }
             }
         }
-        char* dst = y + (int64_t)sp.t * rb;
+    }
+    char* dst = y + (int64_t)sp.t * rb;
 #pragma unroll
-        for (int q = 0; q < PCH; ++q) {
-            const int64_t idx = c0 + q * kWave + lane;
-            if (idx < nch) st16(dst + idx * 16, P::pack(acc[q]));
-        }
+    for (int q = 0; q < PCH; ++q) {
+        const int64_t idx = sp.cb + q * kWave + lane;
+        if (idx < nch) st16_nt(dst + idx * 16, P::pack(acc[q]));
     }
 }
 
@@ -448,6 +492,27 @@ static int pick_pch(int64_t nch)
     if ((dt) == ET_DTYPE_BF16) { constexpr int DT = ET_DTYPE_BF16; __VA_ARGS__; } \
     else { constexpr int DT = ET_DTYPE_F32; __VA_ARGS__; }
 
+#define ET_SWITCH_PCH4(pch, ...)                     \
+    switch (pch) {                                   \
+        case 1: { constexpr int PCH = 1; __VA_ARGS__; } break; \
+        case 2: { constexpr int PCH = 2; __VA_ARGS__; } break; \
+        default: { constexpr int PCH = 4; __VA_ARGS__; } break; \
+    }
+
+// Launches a piece kernel over tokens [0, T) with npieces waves per token and
+// wpb waves per block, in as many launches as keep every launch's wave index
+// below 2^31 (one launch for any realistic shape).
+template <typename F>
+static void for_each_piece_launch(int64_t T, int64_t npieces, int wpb, F&& launch)
+{
+    const int64_t max_tokens = std::max<int64_t>(1, ((int64_t(1) << 31) - wpb) / npieces);
+    for (int64_t t0 = 0; t0 < T; t0 += max_tokens) {
+        const int64_t t1 = std::min<int64_t>(T, t0 + max_tokens);
+        const int64_t waves = (t1 - t0) * npieces;
+        launch(dim3((unsigned)((waves + wpb - 1) / wpb)), (int)t0, (int)t1);
+    }
+}
+
 static dim3 row_grid(int64_t T) { return dim3((unsigned)((T + kRowWaves - 1) / kRowWaves)); }
 
 }  // namespace et
@@ -467,8 +532,11 @@ extern "C" int et_dispatch_fwd(const void* x, int64_t T, int64_t d, int dtype,
     char* xpc = static_cast<char*>(xp);
     if (rb % 16 == 0 && aligned16(x) && aligned16(xp)) {
         const int64_t nch = rb / 16;
-        ET_SWITCH_PCH(pick_pch(nch),
-                      dispatch_fwd_vec<PCH><<<row_grid(T), dim3(kRowThreads), 0, s>>>(xc, (int)T, nch, token_offsets, token_slot, cap, xpc));
+        const int64_t np = (nch + kWave - 1) / kWave;
+        for_each_piece_launch(T, np, kScatterWaves, [&](dim3 grid, int t0, int t1) {
+            dispatch_fwd_vec<<<grid, dim3(kScatterWaves * kWave), 0, s>>>(xc, t0, t1, nch, (uint32_t)np, token_offsets,
+                                                                         token_slot, cap, xpc);
+        });
     } else {
         ET_SWITCH_DT(dtype, dispatch_fwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(xc, (int)T, d, token_offsets, token_slot, cap, xpc));
     }
@@ -488,8 +556,17 @@ static int combine_like(const char* fn, const void* yp, const float* gate, const
     char* yc = static_cast<char*>(y);
     if (rb % 16 == 0 && aligned16(yp) && aligned16(y)) {
         const int64_t nch = rb / 16;
-        ET_SWITCH_DT(dtype, ET_SWITCH_PCH(pick_pch(nch),
-            combine_fwd_vec<DT, PCH><<<row_grid(T), dim3(kRowThreads), 0, s>>>(ypc, gate, (int)T, nch, token_offsets, token_slot, cap, yc)));
+        const int pch = nch <= kWave ? 1 : (nch <= 2 * kWave ? 2 : 4);
+        const int64_t np = (nch + pch * kWave - 1) / (pch * kWave);
+        for_each_piece_launch(T, np, kGatherWaves, [&](dim3 grid, int t0, int t1) {
+            ET_SWITCH_DT(dtype, ET_SWITCH_PCH4(pch,
+                if (gate)
+                    combine_fwd_vec<DT, PCH, true><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
+                        ypc, gate, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap, yc);
+                else
+                    combine_fwd_vec<DT, PCH, false><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
+                        ypc, nullptr, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap, yc)));
+        });
     } else {
         ET_SWITCH_DT(dtype, combine_fwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(ypc, gate, (int)T, d, token_offsets, token_slot, cap, yc));
     }
