@@ -173,13 +173,15 @@ def main() -> int:
     DGATE = torch.empty(S, dtype=torch.float32, device=dev)
     DL = torch.empty(T, E, dtype=torch.float32, device=dev)
     DX = torch.empty(T, d, dtype=act, device=dev)
+    bwsb = et.combine_backward_workspace_bytes(T, S, d, act)
+    BWS = torch.empty(max(bwsb, 1), dtype=torch.uint8, device=dev)
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
     P = [vp(t) for t in (logits, thr, counts, eoff, toff, st, sg, ts, ws, X, XP, YP, Y, DY, DYP, DGATE, DL,
-                         DXP, DX)]
+                         DXP, DX, BWS)]
     (p_lg, p_thr, p_cnt, p_eo, p_to, p_st, p_sg, p_ts, p_ws, p_x, p_xp, p_yp, p_y, p_dy, p_dyp, p_dg, p_dl,
-     p_dxp, p_dx) = P
+     p_dxp, p_dx, p_bws) = P
 
     def stage(i):
         if i == 0:
@@ -189,7 +191,8 @@ def main() -> int:
         elif i == 2:
             rc = lib.et_combine_fwd(p_yp, p_sg, p_to, p_ts, T, d, dt_code, S, p_y, sp)
         elif i == 3:
-            rc = lib.et_combine_bwd(p_dy, p_yp, p_sg, p_to, p_ts, p_eo, T, E, d, dt_code, S, p_dyp, p_dg, p_dl, sp)
+            rc = lib.et_combine_bwd(p_dy, p_yp, p_sg, p_st, p_to, p_ts, p_eo, T, E, d, dt_code, S, p_dyp, p_dg,
+                                    p_dl, p_bws, bwsb, sp)
         else:
             rc = lib.et_dispatch_bwd(p_dxp, p_to, p_ts, T, d, dt_code, S, p_dx, sp)
         if rc != 0:

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 1
+#define ET_ABI_VERSION 2
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -111,19 +111,26 @@ int et_combine_fwd(const void* yp, const float* slot_gate, const int32_t* token_
                    const int32_t* token_slot, int64_t num_tokens, int64_t d, int dtype,
                    int64_t slot_capacity, void* y, void* stream);
 
+/* Bytes of device workspace et_combine_bwd needs: slot_capacity * ceil(d * elem / 1024)
+ * floats when a row is a whole number of 16-byte chunks, else 0. */
+size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype);
+
 /*
  * Combine backward (fused): for every slot s of token t = token(s), expert e:
  *   dYp[s, c]     = cast(slot_gate[s] * dY[t, c])
  *   dgate[s]      = sum_c dY[t, c] * Yp[s, c]            (binary32 accumulate)
  *   dlogits[t, e] = dgate[s] * g * (1 - g), g = slot_gate[s]; 0 elsewhere
- * dlogits (f32 [T, E]) may be NULL; expert_offsets is read only when it is not.
+ * dlogits (f32 [T, E]) may be NULL; sorted_token is read only when it is not.
+ * workspace holds the per-piece partial dot products (et_combine_bwd_workspace_bytes);
+ * it may be NULL when that size is 0.
  * Implements the combine backward of the path (no reference counterpart).
  */
 int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
-                   const int32_t* token_offsets, const int32_t* token_slot,
-                   const int32_t* expert_offsets, int64_t num_tokens, int64_t num_experts,
-                   int64_t d, int dtype, int64_t slot_capacity,
-                   void* dyp, float* dgate, float* dlogits, void* stream);
+                   const int32_t* sorted_token, const int32_t* token_offsets,
+                   const int32_t* token_slot, const int32_t* expert_offsets,
+                   int64_t num_tokens, int64_t num_experts, int64_t d, int dtype,
+                   int64_t slot_capacity, void* dyp, float* dgate, float* dlogits,
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Dispatch backward:  dX[t, c] = cast(sum of dXp[s, c] over t's slots, added in

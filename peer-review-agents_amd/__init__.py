@@ -11,6 +11,7 @@ from .expert_threshold import (  # noqa: F401
     combine,
     combine_autograd,
     combine_backward,
+    combine_backward_workspace_bytes,
     dispatch,
     dispatch_autograd,
     dispatch_backward,

@@ -45,7 +45,9 @@ _SIGNATURES = {
     "et_route": (_int, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _sz, _p]),
     "et_dispatch_fwd": (_int, [_p, _i64, _i64, _int, _p, _p, _i64, _p, _p]),
     "et_combine_fwd": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _i64, _p, _p]),
-    "et_combine_bwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _i64, _p, _p, _p, _p]),
+    "et_combine_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),
+    "et_combine_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _i64, _p, _p, _p, _p, _sz,
+                              _p]),
     "et_dispatch_bwd": (_int, [_p, _p, _p, _i64, _i64, _int, _i64, _p, _p]),
     "et_threshold_workspace_bytes": (_sz, [_i64, _i64]),
     "et_threshold_update": (_int, [_p, _p, _i64, _i64, _i64, _f, _p, _p, _sz, _p]),

@@ -32,19 +32,25 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ float bf16lo(uint32_t w) { return u2f(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return u2f(w & 0xffff0000u); }
 
-// f32 -> bf16, round to nearest even; a NaN keeps sign and top payload and is
-// forced quiet.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
-{
-    uint32_t u = f2u(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x0040u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
+// f32 -> bf16, round to nearest even; a NaN keeps its sign and top payload
+// bits and is forced quiet (bit 6 of the bf16 word).  gfx950's
+// v_cvt_pk_bf16_f32 implements exactly this rule: all 2^32 inputs were checked
+// against the integer formulation
+//     NaN:  (u >> 16) | 0x40      else:  (u + 0x7fff + ((u >> 16) & 1)) >> 16
+// with zero differences (denormals included), so the kernels use the single
+// instruction, which converts two values at once.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
+{
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // ---------------------------------------------------------------------------

@@ -96,20 +96,33 @@ __device__ __forceinline__ void load_thresholds(const float* __restrict__ thr, i
     }
 }
 
-// Logits of UT consecutive tokens starting at tb (NaN past t1 or past E).
+// Logits of UT consecutive tokens starting at tb < t1 (NaN past t1 or past
+// E).  Addresses are clamped into the matrix so that every load is issued
+// unconditionally, all before the first use; a guarded load would complete
+// before the next one issues.
 template <int GM, int UT>
 __device__ __forceinline__ void load_logits(const float* __restrict__ logits, int E, int G, int64_t tb,
                                             int64_t t1, float (&lg)[UT][GM])
 {
     const int lane = lane_id();
 #pragma unroll
-    for (int u = 0; u < UT; ++u)
+    for (int g = 0; g < GM; ++g) {
+        if (g >= G) {
 #pragma unroll
-        for (int g = 0; g < GM; ++g) {
-            const int e = g * kWave + lane;
-            const int64_t t = tb + u;
-            lg[u][g] = (g < G && e < E && t < t1) ? logits[t * E + e] : __builtin_nanf("");
+            for (int u = 0; u < UT; ++u) lg[u][g] = __builtin_nanf("");
+            continue;
         }
+        const int e = g * kWave + lane;
+        const int ec = min(e, E - 1);
+#pragma unroll
+        for (int u = 0; u < UT; ++u) {
+            const int64_t tc = min(tb + u, t1 - 1);
+            lg[u][g] = logits[tc * E + ec];
+        }
+#pragma unroll
+        for (int u = 0; u < UT; ++u)
+            if (e >= E || tb + u >= t1) lg[u][g] = __builtin_nanf("");
+    }
 }
 
 // Selection of one token: m[g] = ballot(score >= thr) over group g, sc[g] =
@@ -235,11 +248,14 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
         int acc[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0;
-        if (ve)
-            for (int r = r0; r < r1; r += 8)
+        const int ec = min(e, E - 1);
+        for (int r = r0; r < r1; r += 8) {
+            int v[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    if (r + i < r1) acc[i] += block_counts[(int64_t)(r + i) * E + e];
+            for (int i = 0; i < 8; ++i) v[i] = block_counts[(int64_t)min(r + i, r1 - 1) * E + ec];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] += (ve && r + i < r1) ? v[i] : 0;
+        }
         int sum = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) sum += acc[i];
@@ -255,7 +271,7 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
             for (int r = r0; r < r1; r += 8) {
                 int v[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = (r + i < r1) ? block_counts[(int64_t)(r + i) * E + e] : 0;
+                for (int i = 0; i < 8; ++i) v[i] = block_counts[(int64_t)min(r + i, r1 - 1) * E + e];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     if (r + i < r1) block_base[(int64_t)(r + i) * E + e] = run;
@@ -269,7 +285,13 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
         const int R = (NB + kScanThreads - 1) / kScanThreads;
         const int r0 = min(NB, tid * R), r1 = min(NB, r0 + R);
         int sum = 0;
-        for (int r = r0; r < r1; ++r) sum += block_slots[r];
+        for (int r = r0; r < r1; r += 8) {
+            int v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = block_slots[min(r + i, r1 - 1)];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += (r + i < r1) ? v[i] : 0;
+        }
         const int incl = wave_incl_scan(sum);
         if (lane == kWave - 1) wtot[wave] = incl;
         __syncthreads();
@@ -311,20 +333,30 @@ __global__ __launch_bounds__(kRouteThreads) void route_fill_kernel(
         const int incl = wave_incl_scan(c);
         const int eo = run + incl - c;
         run += __builtin_amdgcn_readlane(incl, kWave - 1);
-        pos[g] = 0;
-        if (ve) {
-            if (gw == 0) expert_offsets[e] = eo;
-            int base = eo + block_base[(int64_t)b * E + e];
-            for (int w = w0; w < gw; ++w) base += wave_counts[(int64_t)w * E + e];
-            pos[g] = base;
-        }
+        // counts of the earlier waves of this block (all loads issued first)
+        const int ec = min(e, E - 1);
+        int prev[kRouteWaves - 1];
+#pragma unroll
+        for (int i = 0; i < kRouteWaves - 1; ++i)
+            prev[i] = wave_counts[(int64_t)min(w0 + i, gw) * E + ec];
+        int base = eo + block_base[(int64_t)b * E + ec];
+#pragma unroll
+        for (int i = 0; i < kRouteWaves - 1; ++i) base += (w0 + i < gw) ? prev[i] : 0;
+        pos[g] = ve ? base : 0;
+        if (ve && gw == 0) expert_offsets[e] = eo;
     }
     if (gw == 0 && lane == 0) {
         expert_offsets[E] = run;
         token_offsets[T] = run;
     }
     int tok_pos = block_slot_base[b];
-    for (int w = w0; w < gw; ++w) tok_pos += wave_slots[w];
+    {
+        int prev[kRouteWaves - 1];
+#pragma unroll
+        for (int i = 0; i < kRouteWaves - 1; ++i) prev[i] = wave_slots[min(w0 + i, gw)];
+#pragma unroll
+        for (int i = 0; i < kRouteWaves - 1; ++i) tok_pos += (w0 + i < gw) ? prev[i] : 0;
+    }
 
     float th[GM];
     load_thresholds<GM>(thr, E, G, th);

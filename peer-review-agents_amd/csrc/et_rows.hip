@@ -331,91 +331,96 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
     __syncthreads();
 }
 
-template <int DT, int PCH>
-__global__ __launch_bounds__(kRowThreads) void combine_bwd_vec(
-    const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate,
-    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot,
-    const int32_t* __restrict__ eoff, int T, int E, int64_t nch, int64_t cap,
-    char* __restrict__ dyp, float* __restrict__ dgate, float* __restrict__ dlogits)
+// Vector path, pass 1: one wave per 1 KiB piece of a token's row.  For every
+// slot s of the token the wave writes its piece of dYp[s] and the piece's
+// partial dot <dY[t], Yp[s]> (one wave reduction) to part[s * npieces + p].
+// The wave of piece 0 also zero-fills the token's dlogits row; pass 2 then
+// writes the routed entries.
+constexpr int kBwdWaves = 2;
+
+template <int DT>
+__global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
+    const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate, int t_base,
+    int t_end, int64_t nch, uint32_t npieces, const int32_t* __restrict__ tok_off,
+    const int32_t* __restrict__ tok_slot, int64_t cap, int E, char* __restrict__ dyp,
+    float* __restrict__ part, float* __restrict__ dlogits)
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
-    __shared__ int eoff_lds[ET_MAX_EXPERTS + 1];
-    __shared__ float dotbuf[kRowWaves][ET_MAX_EXPERTS];
-    const bool want_dl = dlogits != nullptr;
-    load_eoff_lds(eoff_lds, eoff, E, want_dl);
-    TokenSpan sp;
-    if (!token_span(T, tok_off, cap, sp)) return;
+    PieceSpan sp;
+    if (!piece_span<kBwdWaves>(t_base, t_end, npieces, kWave, tok_off, cap, sp)) return;
     const int lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int64_t idx = sp.cb + lane;
+    const bool on = idx < nch;
     const int64_t rb = nch * 16;
-    const bool multi = nch > (int64_t)PCH * kWave;
-    float dlv[kMaxLanesE];
-#pragma unroll
-    for (int i = 0; i < kMaxLanesE; ++i) dlv[i] = 0.0f;
-
-    const char* dyrow = dy + (int64_t)sp.t * rb;
-    for (int64_t c0 = 0; c0 < nch; c0 += PCH * kWave) {
-        float df[PCH][N];
-#pragma unroll
-        for (int q = 0; q < PCH; ++q) {
-            const int64_t idx = c0 + q * kWave + lane;
-            if (idx < nch) P::unpack(ld16(dyrow + idx * 16), df[q]);
-            else
-#pragma unroll
-                for (int i = 0; i < N; ++i) df[q][i] = 0.0f;
-        }
-        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
-            const int my = load_slot_block(tok_slot, jb, sp.j1);
-            const int n = min(kWave, sp.j1 - jb);
-            for (int u = 0; u < n; ++u) {
-                const int s = __builtin_amdgcn_readlane(my, u);
-                if (s < 0 || (int64_t)s >= cap) continue;
-                const float g = gate[s];
-                const char* src = yp + (int64_t)s * rb;
-                char* dst = dyp + (int64_t)s * rb;
-                v4u w[PCH];
-#pragma unroll
-                for (int q = 0; q < PCH; ++q) {
-                    const int64_t idx = c0 + q * kWave + lane;
-                    if (idx < nch) w[q] = ld16(src + idx * 16);
-                }
-                float part = 0.0f;
-#pragma unroll
-                for (int q = 0; q < PCH; ++q) {
-                    const int64_t idx = c0 + q * kWave + lane;
-                    if (idx < nch) {
-                        float f[N], o[N];
-                        P::unpack(w[q], f);
-#pragma unroll
-                        for (int i = 0; i < N; ++i) {
-                            part = __builtin_fmaf(df[q][i], f[i], part);
-                            o[i] = g * df[q][i];
-                        }
-                        st16(dst + idx * 16, P::pack(o));
-                    }
-                }
-                const float dot = wave_sum(part);
-                if (!multi) {
-                    finish_slot(s, dot, g, dgate, eoff_lds, E, want_dl, dlv);
-                } else if (lane == 0 && jb + u - sp.j0 < ET_MAX_EXPERTS) {
-                    float* slotp = &dotbuf[wave][jb + u - sp.j0];
-                    *slotp = (c0 == 0) ? dot : *slotp + dot;
-                }
-            }
-        }
+    const uint32_t p = (uint32_t)(sp.cb / kWave);
+    if (dlogits && p == 0)
+        for (int e = lane; e < E; e += kWave) dlogits[(int64_t)sp.t * E + e] = 0.0f;
+    float df[N];
+    {
+        v4u w = {0u, 0u, 0u, 0u};
+        if (on) w = ld16(dy + (int64_t)sp.t * rb + idx * 16);
+        P::unpack(w, df);
     }
-    if (multi) {
-        // lane 0 alone wrote dotbuf; it reads back and broadcasts
-        for (int j = sp.j0; j < sp.j1; ++j) {
-            const int s = tok_slot[j];
+    for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+        const int my = load_slot_block(tok_slot, jb, sp.j1);
+        const int n = min(kWave, sp.j1 - jb);
+        for (int u = 0; u < n; ++u) {
+            const int s = __builtin_amdgcn_readlane(my, u);
             if (s < 0 || (int64_t)s >= cap) continue;
-            const float mine = (lane == 0 && j - sp.j0 < ET_MAX_EXPERTS) ? dotbuf[wave][j - sp.j0] : 0.0f;
-            const float dot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mine)));
-            finish_slot(s, dot, gate[s], dgate, eoff_lds, E, want_dl, dlv);
+            const float g = gate[s];
+            v4u w = {0u, 0u, 0u, 0u};
+            if (on) w = ld16(yp + (int64_t)s * rb + idx * 16);
+            float f[N], o[N];
+            P::unpack(w, f);
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                acc = __builtin_fmaf(df[i], f[i], acc);
+                o[i] = g * df[i];
+            }
+            if (on) st16(dyp + (int64_t)s * rb + idx * 16, P::pack(o));
+            const float dot = wave_sum(acc);
+            if (lane == 0) part[(int64_t)s * npieces + p] = dot;
         }
     }
-    if (want_dl) write_dlogits_row(dlogits, sp.t, E, dlv);
+}
+
+// Vector path, pass 2: one thread per slot s < min(expert_offsets[E], cap):
+// dgate[s] = the sum of the slot's partial dots in piece order, and
+// dlogits[sorted_token[s], e(s)] = dgate[s] * g (1 - g), with e(s) found by a
+// binary search of expert_offsets in LDS.
+constexpr int kFinishThreads = 256;
+
+__global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
+    const float* __restrict__ part, uint32_t npieces, const float* __restrict__ gate,
+    const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ eoff, int E, int64_t cap,
+    float* __restrict__ dgate, float* __restrict__ dlogits)
+{
+    extern __shared__ int32_t eo[];                                     // [E + 1]
+    const bool want_dl = dlogits != nullptr;
+    if (want_dl)
+        for (int e = threadIdx.x; e <= E; e += kFinishThreads) eo[e] = eoff[e];
+    __syncthreads();
+    const int64_t s = (int64_t)blockIdx.x * kFinishThreads + threadIdx.x;
+    const int64_t S = min((int64_t)eoff[E], cap);
+    if (s >= S) return;
+    const float* ps = part + s * npieces;
+    float dot = 0.0f;
+    for (uint32_t q0 = 0; q0 < npieces; q0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ps[min(q0 + i, npieces - 1)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (q0 + i < npieces) dot += v[i];
+    }
+    dgate[s] = dot;
+    if (want_dl) {
+        const int e = expert_of_slot(eo, E, (int)s);
+        const float g = gate[s];
+        dlogits[(int64_t)sorted_token[s] * E + e] = dot * (g * (1.0f - g));
+    }
 }
 
 template <int DT>
@@ -469,24 +474,6 @@ static int check_common(const char* fn, int64_t T, int64_t d, int dtype, int64_t
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null token_offsets/token_slot");
     return ET_OK;
 }
-
-// Passes of PCH 16-byte chunks per lane: the smallest PCH in {1,2,4,8} that
-// covers the row in one pass, else 8 (multi-pass).
-static int pick_pch(int64_t nch)
-{
-    if (nch <= 1 * kWave) return 1;
-    if (nch <= 2 * kWave) return 2;
-    if (nch <= 4 * kWave) return 4;
-    return 8;
-}
-
-#define ET_SWITCH_PCH(pch, ...)                      \
-    switch (pch) {                                   \
-        case 1: { constexpr int PCH = 1; __VA_ARGS__; } break; \
-        case 2: { constexpr int PCH = 2; __VA_ARGS__; } break; \
-        case 4: { constexpr int PCH = 4; __VA_ARGS__; } break; \
-        default: { constexpr int PCH = 8; __VA_ARGS__; } break; \
-    }
 
 #define ET_SWITCH_DT(dt, ...)                                          \
     if ((dt) == ET_DTYPE_BF16) { constexpr int DT = ET_DTYPE_BF16; __VA_ARGS__; } \
@@ -587,17 +574,31 @@ extern "C" int et_dispatch_bwd(const void* dxp, const int32_t* token_offsets, co
     return combine_like("et_dispatch_bwd", dxp, nullptr, token_offsets, token_slot, T, d, dtype, cap, dx, stream);
 }
 
+static bool bwd_vector_path(int64_t d, int dtype) { return d > 0 && (d * elem_bytes(dtype)) % 16 == 0; }
+
+extern "C" size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype)
+{
+    (void)num_tokens;
+    if (slot_capacity < 0 || d < 0 || (dtype != ET_DTYPE_F32 && dtype != ET_DTYPE_BF16)) return 0;
+    if (!bwd_vector_path(d, dtype)) return 0;
+    const int64_t nch = d * elem_bytes(dtype) / 16;
+    const int64_t np = (nch + kWave - 1) / kWave;
+    return (size_t)(slot_capacity * np) * sizeof(float);
+}
+
 extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
-                              const int32_t* token_offsets, const int32_t* token_slot,
-                              const int32_t* expert_offsets, int64_t T, int64_t E, int64_t d, int dtype,
-                              int64_t cap, void* dyp, float* dgate, float* dlogits, void* stream)
+                              const int32_t* sorted_token, const int32_t* token_offsets,
+                              const int32_t* token_slot, const int32_t* expert_offsets, int64_t T, int64_t E,
+                              int64_t d, int dtype, int64_t cap, void* dyp, float* dgate, float* dlogits,
+                              void* workspace, size_t workspace_bytes, void* stream)
 {
     if (int rc = check_common("et_combine_bwd", T, d, dtype, cap, token_offsets, token_slot)) return rc;
     if (E < 1 || E > ET_MAX_EXPERTS)
         return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: num_experts must be in [1, " +
                                                  std::to_string(ET_MAX_EXPERTS) + "]");
-    if (dlogits && !expert_offsets)
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: dlogits needs expert_offsets");
+    if (!expert_offsets) return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: null expert_offsets");
+    if (dlogits && cap > 0 && !sorted_token)
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: dlogits needs sorted_token");
     if (T == 0) return ET_OK;
     if (cap > 0 && (!slot_gate || !dgate || (d > 0 && (!dy || !yp || !dyp))))
         return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: null input/output");
@@ -606,12 +607,27 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
     const char* dyc = static_cast<const char*>(dy);
     const char* ypc = static_cast<const char*>(yp);
     char* dypc = static_cast<char*>(dyp);
-    if (d > 0 && rb % 16 == 0 && aligned16(dy) && aligned16(yp) && aligned16(dyp)) {
+    if (bwd_vector_path(d, dtype) && aligned16(dy) && aligned16(yp) && aligned16(dyp)) {
+        const size_t need = et_combine_bwd_workspace_bytes(T, cap, d, dtype);
+        if (need > 0 && (!workspace || workspace_bytes < need))
+            return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_combine_bwd: workspace needs " + std::to_string(need) +
+                                                        " bytes, got " + std::to_string(workspace_bytes));
+        float* part = static_cast<float*>(workspace);
         const int64_t nch = rb / 16;
-        ET_SWITCH_DT(dtype, ET_SWITCH_PCH(pick_pch(nch),
-            combine_bwd_vec<DT, PCH><<<row_grid(T), dim3(kRowThreads), 0, s>>>(dyc, ypc, slot_gate, token_offsets, token_slot, expert_offsets, (int)T, (int)E, nch, cap, dypc, dgate, dlogits)));
-    } else {
-        ET_SWITCH_DT(dtype, combine_bwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(dyc, ypc, slot_gate, token_offsets, token_slot, expert_offsets, (int)T, (int)E, d, cap, dypc, dgate, dlogits));
+        const int64_t np = (nch + kWave - 1) / kWave;
+        for_each_piece_launch(T, np, kBwdWaves, [&](dim3 grid, int t0, int t1) {
+            ET_SWITCH_DT(dtype, combine_bwd_vec<DT><<<grid, dim3(kBwdWaves * kWave), 0, s>>>(
+                                    dyc, ypc, slot_gate, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap,
+                                    (int)E, dypc, part, dlogits));
+        });
+        if (int rc = check_launch("combine_bwd_vec")) return rc;
+        if (cap == 0) return ET_OK;
+        const size_t lds = (size_t)(E + 1) * 4;
+        combine_bwd_finish<<<dim3((unsigned)((cap + kFinishThreads - 1) / kFinishThreads)), dim3(kFinishThreads),
+                             lds, s>>>(part, (uint32_t)np, slot_gate, sorted_token, expert_offsets, (int)E, cap,
+                                       dgate, dlogits);
+        return check_launch("combine_bwd_finish");
     }
+    ET_SWITCH_DT(dtype, combine_bwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(dyc, ypc, slot_gate, token_offsets, token_slot, expert_offsets, (int)T, (int)E, d, cap, dypc, dgate, dlogits));
     return check_launch("et_combine_bwd");
 }

@@ -222,10 +222,17 @@ def combine(yp: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = N
     return y
 
 
+def combine_backward_workspace_bytes(num_tokens: int, slot_capacity: int, d: int,
+                                     dtype: torch.dtype) -> int:
+    return int(lib().et_combine_bwd_workspace_bytes(num_tokens, slot_capacity, d,
+                                                    _ACT_DTYPES[dtype]))
+
+
 def combine_backward(dy: torch.Tensor, yp: torch.Tensor, plan: RoutingPlan, *,
                      need_dlogits: bool = False, out_dyp: Optional[torch.Tensor] = None,
                      out_dgate: Optional[torch.Tensor] = None,
-                     out_dlogits: Optional[torch.Tensor] = None):
+                     out_dlogits: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None):
     """Fused backward of combine.
 
     Returns (dYp [S, d], dgate f32 [S], dlogits f32 [T, E] or None) with
@@ -248,10 +255,17 @@ def combine_backward(dy: torch.Tensor, yp: torch.Tensor, plan: RoutingPlan, *,
     dl = None
     if need_dlogits or out_dlogits is not None:
         dl = _out_or_new(out_dlogits, (T, E), torch.float32, dev, "out_dlogits")
+    wsb = combine_backward_workspace_bytes(T, plan.rows, d, dy.dtype)
+    if workspace is None:
+        workspace = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace must hold {wsb} bytes on {dev}")
     with torch.cuda.device(dev):
-        rc = lib().et_combine_bwd(_vp(dy), _vp(yp), _vp(plan.slot_gate), _vp(plan.token_offsets),
-                                  _vp(plan.token_slot), _vp(plan.expert_offsets), T, E, d, dt,
-                                  plan.rows, _vp(dyp), _vp(dgate), _vp(dl), _stream(dev))
+        rc = lib().et_combine_bwd(_vp(dy), _vp(yp), _vp(plan.slot_gate), _vp(plan.sorted_token),
+                                  _vp(plan.token_offsets), _vp(plan.token_slot),
+                                  _vp(plan.expert_offsets), T, E, d, dt,
+                                  plan.rows, _vp(dyp), _vp(dgate), _vp(dl), _vp(workspace),
+                                  workspace.numel() * workspace.element_size(), _stream(dev))
     check("et_combine_bwd", rc)
     return dyp, dgate, dl
 

@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 10
+    assert len(syms) == 11
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name
@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 1" in hdr
-    assert et.lib().et_abi_version() == 1
+    assert "#define ET_ABI_VERSION 2" in hdr
+    assert et.lib().et_abi_version() == 2
 
 
 def test_workspace_sizes(et):
@@ -69,9 +69,11 @@ def test_row_entry_points_reject_bad_arguments(et):
     assert lib.et_dispatch_fwd(p, 8, 16, 0, None, p, 8, p, None) == ET_ERR_INVALID_ARGUMENT
     assert lib.et_combine_fwd(p, None, p, p, 8, 16, 1, 8, p, None) == ET_ERR_INVALID_ARGUMENT
     assert lib.et_dispatch_bwd(p, p, p, 8, -3, 1, 8, p, None) == ET_ERR_INVALID_ARGUMENT
-    assert lib.et_combine_bwd(p, p, p, p, p, None, 8, 4, 16, 0, 8, p, p, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_combine_bwd(p, p, p, p, p, p, None, 8, 4, 16, 0, 8, p, p, p, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
     assert "expert_offsets" in _err(et)
-    assert lib.et_combine_bwd(p, p, p, p, p, p, 8, 0, 16, 0, 8, p, p, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_combine_bwd(p, p, p, None, p, p, p, 8, 4, 16, 0, 8, p, p, p, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
+    assert "sorted_token" in _err(et)
+    assert lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 0, 16, 0, 8, p, p, p, p, 1 << 20, None) == ET_ERR_INVALID_ARGUMENT
     # zero-size work is a successful no-op that launches nothing
     assert lib.et_dispatch_fwd(p, 0, 16, 0, p, p, 8, p, None) == 0
     assert lib.et_combine_fwd(p, p, p, p, 0, 16, 0, 8, p, None) == 0
@@ -96,3 +98,17 @@ def test_error_string_is_per_call(et):
     first = _err(et)
     lib.et_threshold_update(p, p, 16, 8, 0, 0.99, None, p, 1 << 20, None)
     assert _err(et) != first and "k_target" in _err(et)
+
+
+def test_combine_bwd_workspace(et):
+    lib = et.lib()
+    # one float per slot and 1 KiB piece of the row (C3: d = 4096 bf16 -> 8 pieces)
+    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == 528736 * 8 * 4
+    assert lib.et_combine_bwd_workspace_bytes(4096, 8192, 512, 0) == 8192 * 2 * 4
+    assert lib.et_combine_bwd_workspace_bytes(10, 100, 7, 1) == 0        # element path: none
+    assert lib.et_combine_bwd_workspace_bytes(10, 100, 8, 5) == 0        # bad dtype
+    p = ctypes.c_void_p(0x1000)                   # 16-byte aligned: the vector path is chosen
+    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, None, 0, None)
+    assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "workspace" in _err(et)
+    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, p, 31, None)
+    assert rc == ET_ERR_WORKSPACE_TOO_SMALL
