@@ -200,13 +200,14 @@ __global__ __launch_bounds__(kRowThreads) void dispatch_fwd_elem(
 // ---------------------------------------------------------------------------
 // combine forward: Y[t] = sum_s gate[s] * Yp[s] (fma chain in ascending expert
 // order).  Without GATE this is the dispatch backward dX[t] = sum dXp[s].  One
-// wave per piece of PCH * 64 chunks; the gathered rows are read once and never
+// wave per 1 KiB piece of a token's row: each lane accumulates its 16-byte
+// chunk over the token's slots.  The gathered rows are read once and never
 // again, so loads and the final store are non-temporal.
 // ---------------------------------------------------------------------------
 
-constexpr int kGatherWaves = 4;
+constexpr int kGatherWaves = 2;
 
-template <int DT, int PCH, bool GATE>
+template <int DT, bool GATE>
 __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
     const char* __restrict__ yp, const float* __restrict__ gate, int t_base, int t_end, int64_t nch,
     uint32_t npieces, const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot,
@@ -215,14 +216,13 @@ __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
     using P = Pack<DT>;
     constexpr int N = P::N;
     PieceSpan sp;
-    if (!piece_span<kGatherWaves>(t_base, t_end, npieces, PCH * kWave, tok_off, cap, sp)) return;
-    const int lane = lane_id();
+    if (!piece_span<kGatherWaves>(t_base, t_end, npieces, kWave, tok_off, cap, sp)) return;
+    const int64_t idx = sp.cb + lane_id();
+    const bool on = idx < nch;
     const int64_t rb = nch * 16;
-    float acc[PCH][N];
+    float acc[N];
 #pragma unroll
-    for (int q = 0; q < PCH; ++q)
-#pragma unroll
-        for (int i = 0; i < N; ++i) acc[q][i] = 0.0f;
+    for (int i = 0; i < N; ++i) acc[i] = 0.0f;
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
         const int my = load_slot_block(tok_slot, jb, sp.j1);
         const int n = min(kWave, sp.j1 - jb);
@@ -230,31 +230,15 @@ __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
             const int s = __builtin_amdgcn_readlane(my, u);
             if (s < 0 || (int64_t)s >= cap) continue;
             const float g = GATE ? gate[s] : 1.0f;
-            const char* src = yp + (int64_t)s * rb;
-            v4u w[PCH];
+            if (on) {
+                float f[N];
+                P::unpack(ld16_nt(yp + (int64_t)s * rb + idx * 16), f);
 #pragma unroll
-            for (int q = 0; q < PCH; ++q) {
-                const int64_t idx = sp.cb + q * kWave + lane;
-                if (idx < nch) w[q] = ld16_nt(src + idx * 16);
-            }
-#pragma unroll
-            for (int q = 0; q < PCH; ++q) {
-                const int64_t idx = sp.cb + q * kWave + lane;
-                if (idx < nch) {
-                    float f[N];
-                    P::unpack(w[q], f);
-#pragma unroll
-                    for (int i = 0; i < N; ++i) acc[q][i] = __builtin_fmaf(g, f[i], acc[q][i]);
-                }
+                for (int i = 0; i < N; ++i) acc[i] = __builtin_fmaf(g, f[i], acc[i]);
             }
         }
     }
-    char* dst = y + (int64_t)sp.t * rb;
-#pragma unroll
-    for (int q = 0; q < PCH; ++q) {
-        const int64_t idx = sp.cb + q * kWave + lane;
-        if (idx < nch) st16_nt(dst + idx * 16, P::pack(acc[q]));
-    }
+    if (on) st16_nt(y + (int64_t)sp.t * rb + idx * 16, P::pack(acc));
 }
 
 template <int DT>
@@ -479,13 +463,6 @@ static int check_common(const char* fn, int64_t T, int64_t d, int dtype, int64_t
     if ((dt) == ET_DTYPE_BF16) { constexpr int DT = ET_DTYPE_BF16; __VA_ARGS__; } \
     else { constexpr int DT = ET_DTYPE_F32; __VA_ARGS__; }
 
-#define ET_SWITCH_PCH4(pch, ...)                     \
-    switch (pch) {                                   \
-        case 1: { constexpr int PCH = 1; __VA_ARGS__; } break; \
-        case 2: { constexpr int PCH = 2; __VA_ARGS__; } break; \
-        default: { constexpr int PCH = 4; __VA_ARGS__; } break; \
-    }
-
 // Launches a piece kernel over tokens [0, T) with npieces waves per token and
 // wpb waves per block, in as many launches as keep every launch's wave index
 // below 2^31 (one launch for any realistic shape).
@@ -543,16 +520,15 @@ static int combine_like(const char* fn, const void* yp, const float* gate, const
     char* yc = static_cast<char*>(y);
     if (rb % 16 == 0 && aligned16(yp) && aligned16(y)) {
         const int64_t nch = rb / 16;
-        const int pch = nch <= kWave ? 1 : (nch <= 2 * kWave ? 2 : 4);
-        const int64_t np = (nch + pch * kWave - 1) / (pch * kWave);
+        const int64_t np = (nch + kWave - 1) / kWave;
         for_each_piece_launch(T, np, kGatherWaves, [&](dim3 grid, int t0, int t1) {
-            ET_SWITCH_DT(dtype, ET_SWITCH_PCH4(pch,
+            ET_SWITCH_DT(dtype,
                 if (gate)
-                    combine_fwd_vec<DT, PCH, true><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
+                    combine_fwd_vec<DT, true><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
                         ypc, gate, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap, yc);
                 else
-                    combine_fwd_vec<DT, PCH, false><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
-                        ypc, nullptr, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap, yc)));
+                    combine_fwd_vec<DT, false><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
+                        ypc, nullptr, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap, yc));
         });
     } else {
         ET_SWITCH_DT(dtype, combine_fwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(ypc, gate, (int)T, d, token_offsets, token_slot, cap, yc));
