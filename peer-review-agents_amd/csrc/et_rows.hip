@@ -315,11 +315,12 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
     __syncthreads();
 }
 
-// Vector path, pass 1: one wave per 1 KiB piece of a token's row.  For every
-// slot s of the token the wave writes its piece of dYp[s] and the piece's
-// partial dot <dY[t], Yp[s]> (one wave reduction) to part[s * npieces + p].
-// The wave of piece 0 also zero-fills the token's dlogits row; pass 2 then
-// writes the routed entries.
+// Vector path, pass 1: one wave per 1 KiB piece of a token's row.
+// For every slot s of the token the wave writes its piece of dYp[s] and the
+// piece's partial dot <dY[t], Yp[s]> (one wave reduction) to
+// part[s * npieces + p].  Yp is read once and dYp written once, both
+// non-temporal.  The wave of piece 0 also zero-fills the token's dlogits row;
+// pass 2 then writes the routed entries.
 constexpr int kBwdWaves = 2;
 
 template <int DT>
@@ -354,7 +355,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
             if (s < 0 || (int64_t)s >= cap) continue;
             const float g = gate[s];
             v4u w = {0u, 0u, 0u, 0u};
-            if (on) w = ld16(yp + (int64_t)s * rb + idx * 16);
+            if (on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
             float f[N], o[N];
             P::unpack(w, f);
             float acc = 0.0f;
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
                 acc = __builtin_fmaf(df[i], f[i], acc);
                 o[i] = g * df[i];
             }
-            if (on) st16(dyp + (int64_t)s * rb + idx * 16, P::pack(o));
+            if (on) st16_nt(dyp + (int64_t)s * rb + idx * 16, P::pack(o));
             const float dot = wave_sum(acc);
             if (lane == 0) part[(int64_t)s * npieces + p] = dot;
         }
