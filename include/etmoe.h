@@ -28,11 +28,15 @@
  *  - Index arrays are int32: T*E must stay below 2^31.
  *  - `slot_capacity` is the allocated length of the slot arrays (sorted_token,
  *    slot_gate, token_slot, dgate) and the row count of the slot-major
- *    activation buffers (Xp, Yp, dYp, dXp).  Routing never writes a slot index
- *    >= slot_capacity, and the row kernels skip such slots, so an undersized
- *    buffer loses data but is never written out of bounds.  T*E is always a
- *    sufficient capacity.  The number of routed slots S is expert_offsets[E]
- *    (also token_offsets[T]); compare it with the capacity after routing.
+ *    activation buffers (Xp, Yp, dYp, dXp).  T*E is always a sufficient
+ *    capacity.  The number of routed slots S is expert_offsets[E] (also
+ *    token_offsets[T]); compare it with the capacity after routing.  With an
+ *    undersized capacity nothing is written out of bounds and data is lost:
+ *    a routed pair is kept only if both its slot index and its entry in the
+ *    token-major list are below the capacity.  The row kernels skip every
+ *    other pair, so combine and dispatch backward sum the kept pairs only,
+ *    dlogits is 0 at dropped pairs, and the rows of dropped slots below the
+ *    capacity are left as they were (their dgate is 0 or left as it was).
  *  - Concurrent calls on different streams are safe when their buffers are
  *    disjoint (the library keeps no device state).
  */
@@ -120,7 +124,7 @@ size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity,
  *   dYp[s, c]     = cast(slot_gate[s] * dY[t, c])
  *   dgate[s]      = sum_c dY[t, c] * Yp[s, c]            (binary32 accumulate)
  *   dlogits[t, e] = dgate[s] * g * (1 - g), g = slot_gate[s]; 0 elsewhere
- * dlogits (f32 [T, E]) may be NULL; sorted_token is read only when it is not.
+ * dlogits (f32 [T, E]) may be NULL.
  * workspace holds the per-piece partial dot products (et_combine_bwd_workspace_bytes);
  * it may be NULL when that size is 0.
  * Implements the combine backward of the path (no reference counterpart).

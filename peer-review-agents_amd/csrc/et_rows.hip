@@ -374,12 +374,15 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
 // Vector path, pass 2: one thread per slot s < min(expert_offsets[E], cap):
 // dgate[s] = the sum of the slot's partial dots in piece order, and
 // dlogits[sorted_token[s], e(s)] = dgate[s] * g (1 - g), with e(s) found by a
-// binary search of expert_offsets in LDS.
+// binary search of expert_offsets in LDS.  A slot that pass 1 skipped (its
+// token-list entry at or past an undersized capacity) gets dgate 0 and leaves
+// its dlogits entry at the zero pass 1 wrote.
 constexpr int kFinishThreads = 256;
 
 __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
     const float* __restrict__ part, uint32_t npieces, const float* __restrict__ gate,
-    const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ eoff, int E, int64_t cap,
+    const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ tok_off,
+    const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff, int E, int64_t cap,
     float* __restrict__ dgate, float* __restrict__ dlogits)
 {
     extern __shared__ int32_t eo[];                                     // [E + 1]
@@ -390,6 +393,19 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
     const int64_t s = (int64_t)blockIdx.x * kFinishThreads + threadIdx.x;
     const int64_t S = min((int64_t)eoff[E], cap);
     if (s >= S) return;
+    if ((int64_t)eoff[E] > cap) {
+        // Undersized capacity: pass 1 skipped slot s unless its token-list
+        // entry is also below the capacity.  Only the token whose list
+        // straddles the capacity needs a search.
+        const int t = sorted_token[s];
+        const int64_t a = tok_off[t], b = tok_off[t + 1];
+        bool kept = b <= cap;
+        for (int64_t j = a; !kept && j < cap && j < b; ++j) kept = tok_slot[j] == (int32_t)s;
+        if (!kept) {
+            dgate[s] = 0.0f;
+            return;
+        }
+    }
     const float* ps = part + s * npieces;
     float dot = 0.0f;
     for (uint32_t q0 = 0; q0 < npieces; q0 += 8) {
@@ -574,8 +590,7 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
         return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: num_experts must be in [1, " +
                                                  std::to_string(ET_MAX_EXPERTS) + "]");
     if (!expert_offsets) return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: null expert_offsets");
-    if (dlogits && cap > 0 && !sorted_token)
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: dlogits needs sorted_token");
+    if (cap > 0 && !sorted_token) return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: null sorted_token");
     if (T == 0) return ET_OK;
     if (cap > 0 && (!slot_gate || !dgate || (d > 0 && (!dy || !yp || !dyp))))
         return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: null input/output");
@@ -601,8 +616,8 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
         if (cap == 0) return ET_OK;
         const size_t lds = (size_t)(E + 1) * 4;
         combine_bwd_finish<<<dim3((unsigned)((cap + kFinishThreads - 1) / kFinishThreads)), dim3(kFinishThreads),
-                             lds, s>>>(part, (uint32_t)np, slot_gate, sorted_token, expert_offsets, (int)E, cap,
-                                       dgate, dlogits);
+                             lds, s>>>(part, (uint32_t)np, slot_gate, sorted_token, token_offsets, token_slot,
+                                       expert_offsets, (int)E, cap, dgate, dlogits);
         return check_launch("combine_bwd_finish");
     }
     ET_SWITCH_DT(dtype, combine_bwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(dyc, ypc, slot_gate, token_offsets, token_slot, expert_offsets, (int)T, (int)E, d, cap, dypc, dgate, dlogits));

@@ -312,3 +312,52 @@ def test_threshold_dynamics_c5(et, orc, dev):
         np.testing.assert_array_equal(bits(host(router.thr)), bits(thr_o))
         assert plan.num_slots >= T
     assert fallback_tokens > 0                    # the zero-expert fallback was exercised
+
+
+def test_rows_with_undersized_capacity(et, orc, dev):
+    """With slot_capacity below S, a routed pair is kept only if both its slot
+    and its token-list entry are below the capacity; the row kernels skip every
+    other pair and write nothing past the capacity.  Expected values: the
+    oracle on the full routing, at the kept pairs; combine and dispatch
+    backward from the oracle on the token lists with the dropped pairs removed."""
+    lib = et.lib()
+    T, E, d = 500, 12, 72
+    lg, thr = synthetic_router(T, E, "quantile", seed=21)
+    full = orc.route(lg, thr)
+    S = full.num_slots
+    cap = S * 2 // 3
+    plan = et.route(dev_f32(lg, dev), dev_f32(thr, dev), slot_capacity=cap)
+    torch.cuda.synchronize()
+    assert int(plan.expert_offsets[E]) == S
+    entry = np.arange(S)
+    keep_entry = (full.token_slot < cap) & (entry < cap)          # token-major entries kept
+    kept_slot = np.zeros(S, bool)
+    kept_slot[full.token_slot[keep_entry]] = True                 # slot-major: kept slots
+    kept_before = np.concatenate([[0], np.cumsum(keep_entry)])
+    r_kept = orc.Routing(full.counts, full.expert_offsets, kept_before[full.token_offsets].astype(np.int32),
+                         full.sorted_token, full.slot_gate, full.token_slot[keep_entry].astype(np.int32))
+    x, yp, dy, dxp = make_rows(orc, full, T, d, "bf16", seed=4)
+    X, YP, DY, DXP = (to_dev(a, dev) for a in (x, yp[:cap], dy, dxp[:cap]))
+    ks = np.nonzero(kept_slot[:cap])[0]
+    assert 0 < len(ks) < cap                                      # some slots below cap are dropped too
+
+    guard = 8
+    xp = torch.full((cap + guard, d), 7.0, device=dev).to(torch.bfloat16)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    rc = lib.et_dispatch_fwd(vp(X), T, d, 1, vp(plan.token_offsets), vp(plan.token_slot), cap, vp(xp),
+                             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(xp)[ks], x[full.sorted_token[ks]])
+    assert bool((xp[cap:].float() == 7.0).all())                  # nothing past the capacity
+    np.testing.assert_array_equal(bits(host(et.combine(YP, plan))), bits(orc.combine_fwd(yp, r_kept, T)))
+    np.testing.assert_array_equal(bits(host(et.dispatch_backward(DXP, plan))), bits(orc.dispatch_bwd(dxp, r_kept, T)))
+
+    dyp_g, dgate_g, dl_g = et.combine_backward(DY, YP, plan, need_dlogits=True)
+    dyp_o, dgate_o, dl_o = orc.combine_bwd(dy, yp, full, E, want_dlogits=True)
+    np.testing.assert_array_equal(host(dyp_g)[ks], dyp_o[ks])
+    np.testing.assert_allclose(host(dgate_g)[ks], dgate_o[ks], rtol=1e-4, atol=1e-6)
+    ee = np.repeat(np.arange(E), np.diff(full.expert_offsets))
+    want_dl = np.zeros((T, E), np.float32)
+    want_dl[full.sorted_token[kept_slot], ee[kept_slot]] = dl_o[full.sorted_token[kept_slot], ee[kept_slot]]
+    np.testing.assert_allclose(host(dl_g), want_dl, rtol=1e-4, atol=1e-7)
