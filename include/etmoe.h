@@ -145,7 +145,8 @@ int et_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const int32_t
                     int64_t num_tokens, int64_t d, int dtype, int64_t slot_capacity,
                     void* dx, void* stream);
 
-/* Bytes of device workspace et_threshold_update needs for E experts. */
+/* Bytes of device workspace et_threshold_update needs for T tokens and E experts
+ * (it holds the T*E score keys and the radix-select histograms). */
 size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 
 /*

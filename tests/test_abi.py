@@ -34,7 +34,7 @@ def test_workspace_sizes(et):
     assert lib.et_route_workspace_bytes(65536, 128) >= 2 * 256 * 128 * 4
     assert lib.et_route_workspace_bytes(0, 8) > 0
     assert lib.et_route_workspace_bytes(10, 0) == 0
-    assert lib.et_threshold_workspace_bytes(131072, 64) >= 64 * 256 * 4
+    assert lib.et_threshold_workspace_bytes(131072, 64) >= 64 * 256 * 4 + 131072 * 64 * 4
     assert lib.et_threshold_workspace_bytes(10, 0) == 0
 
 
