@@ -3,15 +3,17 @@
 // 8-bit MSB-first radix select over the score bits, then
 // thr[e] = fma(momentum, thr[e], (1 - momentum) * stat[e]).
 //
-// The first histogram pass computes every score key once (lane = expert,
-// coalesced reads of the logits) and stores the keys; the three later passes
-// read the keys.  Per-block histograms live in LDS laid out [digit][lane], so
-// a wave's 64 updates land in distinct banks, and are added into the global
-// histogram with atomics on the non-zero bins (integer counts: the result does
-// not depend on their order).  Each block adds into one of kHistReplicas
-// copies of the histogram (block index modulo the count), which divides the
-// number of atomics that contend for one address; the select pass sums the
-// copies.
+// Four passes, one per 8-bit digit, each a histogram launch and a select
+// launch; no global atomics, so the result is deterministic by construction.
+//   histogram: grid (token blocks, 64-expert groups), 16 waves per block,
+//     lane = expert (coalesced 256-byte row segments).  The first pass reads
+//     the logits, computes every score key once and stores the keys; the later
+//     passes read the keys.  A block counts the digits of the keys that match
+//     the prefix fixed so far in an LDS histogram and writes it whole to
+//     partial[group][block][lane][digit].
+//   select: one block per expert sums the expert's partial histograms, finds
+//     the digit that holds the rank-th largest matching key, and narrows the
+//     prefix and the rank for the next pass.
 #include <algorithm>
 
 #include "et_common.hpp"
@@ -20,61 +22,84 @@ namespace et {
 
 static inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-// ---------------------------------------------------------------------------
-// EMA threshold update: exact per-expert c-th largest score by 4 passes of an
-// 8-bit MSB-first radix select on the score bits, then the EMA.
-// ---------------------------------------------------------------------------
-
 constexpr int kThrThreads = 256;
-constexpr int kHistReplicas = 8;
+constexpr int kHistWaves = 16;
+constexpr int kHistThreads = kHistWaves * kWave;
+constexpr int64_t kHistBlocksFirst = 256;   // blocks of the score pass (whole grid)
+constexpr int kHistUTFirst = 8;             // tokens in flight per wave, score pass
+constexpr int64_t kHistBlocksKeys = 128;    // blocks of the key passes (whole grid)
+constexpr int kHistUTKeys = 16;             // tokens in flight per wave, key passes
+constexpr int64_t kMaxTokensPerBlock = 65535;  // LDS counts are 16-bit
+constexpr int kPitch = kWave + 1;           // LDS words per digit pair (padded)
+constexpr int kHistSize = kWave * 256;      // counts in one block histogram
+constexpr int kSelectThreads = 1024;
+constexpr int kSelectSplit = kSelectThreads / 256;
+
+// Token blocks per 64-expert group of a histogram pass.
+struct HistGrid {
+    int64_t blocks;  // token blocks per group
+    int64_t tpb;     // tokens per block
+};
+
+static HistGrid hist_grid(int64_t T, int64_t E, int64_t target_blocks, int ut)
+{
+    const int64_t groups = (E + kWave - 1) / kWave;
+    HistGrid g;
+    int64_t b = std::max<int64_t>(1, target_blocks / groups);
+    b = std::max<int64_t>(b, (T + kMaxTokensPerBlock - 1) / kMaxTokensPerBlock);
+    g.tpb = std::max<int64_t>(1, (T + b - 1) / b);
+    g.tpb = std::max<int64_t>(g.tpb, (int64_t)kHistWaves * ut);
+    g.tpb = std::min<int64_t>(g.tpb, kMaxTokensPerBlock);
+    g.blocks = std::max<int64_t>(1, (T + g.tpb - 1) / g.tpb);
+    return g;
+}
 
 struct ThrWs {
-    uint32_t* prefix;  // [E]  bits of the selected key fixed so far
-    uint32_t* rank;    // [E]  rank still to find among keys matching prefix
-    uint32_t* hist;    // [kHistReplicas][E][256]
-    uint32_t* keys;    // [T * E] score keys (bit patterns of the scores; NaN -> 0)
+    uint32_t* prefix;   // [E]  bits of the selected key fixed so far
+    uint32_t* rank;     // [E]  rank still to find among keys matching prefix
+    uint32_t* keys;     // [T * E] score keys (bit patterns of the scores; NaN -> 0)
+    uint32_t* partial;  // [groups][blocks][64][256] block histograms of one pass
+    HistGrid g1, g2;    // grids of the score pass and of the key passes
     size_t bytes;
 };
 
 static ThrWs thr_ws_layout(void* base, int64_t T, int64_t E)
 {
     ThrWs ws{};
+    ws.g1 = hist_grid(T, E, kHistBlocksFirst, kHistUTFirst);
+    ws.g2 = hist_grid(T, E, kHistBlocksKeys, kHistUTKeys);
+    const int64_t groups = (E + kWave - 1) / kWave;
+    const int64_t nb = std::max(ws.g1.blocks, ws.g2.blocks);
     size_t off = 0;
     char* b = static_cast<char*>(base);
     ws.prefix = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(E) * 4);
     ws.rank = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(E) * 4);
-    ws.hist = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(kHistReplicas) * E * 256 * 4);
     ws.keys = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(T * E) * 4);
+    ws.partial = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(groups * nb) * kHistSize * 4);
     ws.bytes = off;
     return ws;
 }
 
-__global__ __launch_bounds__(kThrThreads) void thr_init_kernel(int E, uint32_t c, uint32_t* prefix,
-                                                               uint32_t* rank, uint32_t* hist)
+__global__ __launch_bounds__(kThrThreads) void thr_init_kernel(int E, uint32_t c, uint32_t* prefix, uint32_t* rank)
 {
-    const int64_t i = (int64_t)blockIdx.x * kThrThreads + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kThrThreads;
+    const int i = blockIdx.x * kThrThreads + threadIdx.x;
     if (i < E) { prefix[i] = 0u; rank[i] = c; }
-    for (int64_t j = i; j < (int64_t)kHistReplicas * E * 256; j += stride) hist[j] = 0u;
 }
 
-// One digit-histogram pass.  Grid (token blocks, 64-expert groups), 16 waves
-// per block; lane = expert.  Each wave takes UT consecutive tokens at a time,
+// One digit-histogram pass.  Each wave takes UT consecutive tokens at a time,
 // with all UT loads issued before the first use (addresses clamped into the
-// matrix).  FIRST: the input is the logits; the key of every score is stored.
-// Otherwise the input is the stored keys.
-constexpr int kHistWaves = 16;
-constexpr int kHistThreads = kHistWaves * kWave;
-constexpr int kHistUT = 8;
-
-template <bool FIRST>
+// matrix).  FIRST: the input is the logits and the key of every score is
+// stored; otherwise the input is the stored keys.  LDS counts are 16-bit, two
+// digits to a word (word (d >> 1) * kPitch + lane, half d & 1); a block covers
+// at most 65535 tokens, so a half never carries into its neighbour.
+template <bool FIRST, int UT>
 __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
     const float* __restrict__ logits, uint32_t* __restrict__ keys, int T, int E, int shift,
-    int tokens_per_block, const uint32_t* __restrict__ prefix, uint32_t* __restrict__ hist)
+    int tokens_per_block, const uint32_t* __restrict__ prefix, uint32_t* __restrict__ partial)
 {
-    __shared__ uint32_t h[256 * kWave];
+    __shared__ uint32_t h[128 * kPitch];
     const int tid = threadIdx.x;
-    for (int i = tid; i < 256 * kWave; i += kHistThreads) h[i] = 0u;
+    for (int i = tid; i < 128 * kPitch; i += kHistThreads) h[i] = 0u;
     __syncthreads();
     const int lane = lane_id();
     const int wave = tid >> 6;
@@ -85,15 +110,15 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
     const uint32_t pre = prefix[ec] & hmask;
     const int64_t t0 = (int64_t)blockIdx.x * tokens_per_block;
     const int64_t t1 = min((int64_t)T, t0 + tokens_per_block);
-    for (int64_t tb = t0 + (int64_t)wave * kHistUT; tb < t1; tb += (int64_t)kHistWaves * kHistUT) {
-        uint32_t v[kHistUT];
+    for (int64_t tb = t0 + (int64_t)wave * UT; tb < t1; tb += (int64_t)kHistWaves * UT) {
+        uint32_t v[UT];
 #pragma unroll
-        for (int u = 0; u < kHistUT; ++u) {
+        for (int u = 0; u < UT; ++u) {
             const int64_t tc = min(tb + u, t1 - 1);
             v[u] = FIRST ? f2u(logits[tc * E + ec]) : keys[tc * E + ec];
         }
 #pragma unroll
-        for (int u = 0; u < kHistUT; ++u) {
+        for (int u = 0; u < UT; ++u) {
             const int64_t t = tb + u;
             if (!ve || t >= t1) continue;
             uint32_t key = v[u];
@@ -102,48 +127,60 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
                 key = (sc != sc) ? 0u : f2u(sc);
                 keys[t * E + e] = key;
             }
-            if ((key & hmask) == pre) atomicAdd(&h[((key >> shift) & 255u) * kWave + lane], 1u);
+            if ((key & hmask) == pre) {
+                const uint32_t d = (key >> shift) & 255u;
+                atomicAdd(&h[(d >> 1) * kPitch + lane], 1u << ((d & 1u) * 16));
+            }
         }
     }
     __syncthreads();
-    uint32_t* hr = hist + (int64_t)(blockIdx.x % kHistReplicas) * E * 256;
-    for (int i = tid; i < 256 * kWave; i += kHistThreads) {
-        const uint32_t v = h[i];
-        const int ee = blockIdx.y * kWave + (i & (kWave - 1));
-        if (v != 0u && ee < E) atomicAdd(&hr[(int64_t)ee * 256 + (i >> 6)], v);
+    uint32_t* out = partial + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kHistSize;
+    for (int i = tid; i < kHistSize; i += kHistThreads) {
+        const int l = i >> 8, d = i & 255;
+        out[i] = (h[(d >> 1) * kPitch + l] >> ((d & 1) * 16)) & 0xffffu;
     }
 }
 
-// one wave per expert: find the digit holding the rank-th largest key, update
-// prefix and rank, and clear the expert's histogram for the next pass.
-__global__ __launch_bounds__(kThrThreads) void thr_select_kernel(int E, int shift,
-                                                                 uint32_t* __restrict__ prefix,
-                                                                 uint32_t* __restrict__ rank,
-                                                                 uint32_t* __restrict__ hist)
+// One block per expert: counts[d] = the sum of the expert's block histograms
+// (kSelectSplit threads per digit, each over every kSelectSplit-th block, all
+// loads of a round issued together), then one wave walks the digits from the
+// top to the one holding the rank-th largest matching key.
+__global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
+    int E, int shift, int nblocks, const uint32_t* __restrict__ partial, uint32_t* __restrict__ prefix,
+    uint32_t* __restrict__ rank)
 {
-    const int lane = lane_id();
-    const int e = blockIdx.x * (kThrThreads / kWave) + (threadIdx.x >> 6);
-    if (e >= E) return;
-    // position p = 4*lane + i walks the bins from the top: bin = 255 - p; each
-    // count is the sum over the histogram copies
+    __shared__ uint32_t part[kSelectSplit][256];
+    const int e = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int q = tid >> 8, d = tid & 255;
+    const uint32_t* src = partial + (int64_t)(e >> 6) * nblocks * kHistSize + (e & 63) * 256 + d;
+    uint32_t sum = 0u;
+    for (int b0 = q; b0 < nblocks; b0 += 8 * kSelectSplit) {
+        uint32_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = src[(int64_t)min(b0 + i * kSelectSplit, nblocks - 1) * kHistSize];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += (b0 + i * kSelectSplit < nblocks) ? v[i] : 0u;
+    }
+    part[q][d] = sum;
+    __syncthreads();
+    if (tid >= kWave) return;
+    const int lane = tid;
+    // position p = 4*lane + i walks the bins from the top: bin = 255 - p
     uint32_t c[4];
     int tot = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        uint32_t v[kHistReplicas];
-#pragma unroll
-        for (int r = 0; r < kHistReplicas; ++r) v[r] = hist[((int64_t)r * E + e) * 256 + 255 - (4 * lane + i)];
+        const int bin = 255 - (4 * lane + i);
         c[i] = 0u;
 #pragma unroll
-        for (int r = 0; r < kHistReplicas; ++r) c[i] += v[r];
+        for (int k = 0; k < kSelectSplit; ++k) c[i] += part[k][bin];
         tot += (int)c[i];
     }
     const int incl = wave_incl_scan(tot);
     const int excl = incl - tot;
     const int r = (int)rank[e];
-    const bool mine = excl < r && r <= incl;
-    const uint64_t who = __ballot(mine);
-    if (mine) {
+    if (excl < r && r <= incl) {
         int run = excl;
         int pos = 4 * lane + 3;
 #pragma unroll
@@ -155,11 +192,6 @@ __global__ __launch_bounds__(kThrThreads) void thr_select_kernel(int E, int shif
         prefix[e] = prefix[e] | (bin << shift);
         rank[e] = (uint32_t)(r - run);
     }
-    (void)who;
-#pragma unroll
-    for (int r = 0; r < kHistReplicas; ++r)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) hist[((int64_t)r * E + e) * 256 + 255 - (4 * lane + i)] = 0u;
 }
 
 __global__ __launch_bounds__(kThrThreads) void thr_finalize_kernel(int E, const uint32_t* __restrict__ prefix,
@@ -211,26 +243,23 @@ extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, i
     if (c > T) c = T;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int Ti = (int)T, Ei = (int)E;
+    const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
 
-    const int init_blocks = (int)std::min<int64_t>((E * 256 + kThrThreads - 1) / kThrThreads, 1024);
-    thr_init_kernel<<<dim3(init_blocks), dim3(kThrThreads), 0, s>>>(Ei, (uint32_t)c, ws.prefix, ws.rank, ws.hist);
+    thr_init_kernel<<<dim3((Ei + kThrThreads - 1) / kThrThreads), dim3(kThrThreads), 0, s>>>(Ei, (uint32_t)c, ws.prefix, ws.rank);
     if (int rc = check_launch("thr_init_kernel")) return rc;
-
-    // about one 1024-thread block per CU over the whole grid
-    const int egroups = (Ei + kWave - 1) / kWave;
-    int64_t tblocks = std::max<int64_t>(1, 256 / egroups);
-    int64_t tpb = (T + tblocks - 1) / tblocks;
-    tpb = std::max<int64_t>(tpb, (int64_t)kHistWaves * kHistUT);
-    tblocks = (T + tpb - 1) / tpb;
-    const dim3 grid((unsigned)tblocks, egroups);
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
+        const HistGrid& g = pass == 0 ? ws.g1 : ws.g2;
+        const dim3 grid((unsigned)g.blocks, groups);
         if (pass == 0)
-            thr_hist_kernel<true><<<grid, dim3(kHistThreads), 0, s>>>(logits, ws.keys, Ti, Ei, shift, (int)tpb, ws.prefix, ws.hist);
+            thr_hist_kernel<true, kHistUTFirst><<<grid, dim3(kHistThreads), 0, s>>>(
+                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial);
         else
-            thr_hist_kernel<false><<<grid, dim3(kHistThreads), 0, s>>>(logits, ws.keys, Ti, Ei, shift, (int)tpb, ws.prefix, ws.hist);
+            thr_hist_kernel<false, kHistUTKeys><<<grid, dim3(kHistThreads), 0, s>>>(
+                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial);
         if (int rc = check_launch("thr_hist_kernel")) return rc;
-        thr_select_kernel<<<dim3((Ei + 3) / 4), dim3(kThrThreads), 0, s>>>(Ei, shift, ws.prefix, ws.rank, ws.hist);
+        thr_select_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(Ei, shift, (int)g.blocks, ws.partial,
+                                                                   ws.prefix, ws.rank);
         if (int rc = check_launch("thr_select_kernel")) return rc;
     }
     thr_finalize_kernel<<<dim3((Ei + kThrThreads - 1) / kThrThreads), dim3(kThrThreads), 0, s>>>(Ei, ws.prefix, thr, stat, momentum);
