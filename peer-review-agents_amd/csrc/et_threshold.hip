@@ -4,7 +4,8 @@
 // thr[e] = fma(momentum, thr[e], (1 - momentum) * stat[e]).
 //
 // Four passes, one per 8-bit digit, each a histogram launch and a select
-// launch; no global atomics, so the result is deterministic by construction.
+// launch (the last select also applies the EMA); no global atomics, so the
+// result is deterministic by construction.
 //   histogram: grid (token blocks, 64-expert groups), 16 waves per block,
 //     lane = expert (coalesced 256-byte row segments).  The first pass reads
 //     the logits, computes every score key once and stores the keys; the later
@@ -22,7 +23,6 @@ namespace et {
 
 static inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-constexpr int kThrThreads = 256;
 constexpr int kHistWaves = 16;
 constexpr int kHistThreads = kHistWaves * kWave;
 constexpr int64_t kHistBlocksFirst = 256;   // blocks of the score pass (whole grid)
@@ -80,12 +80,6 @@ static ThrWs thr_ws_layout(void* base, int64_t T, int64_t E)
     return ws;
 }
 
-__global__ __launch_bounds__(kThrThreads) void thr_init_kernel(int E, uint32_t c, uint32_t* prefix, uint32_t* rank)
-{
-    const int i = blockIdx.x * kThrThreads + threadIdx.x;
-    if (i < E) { prefix[i] = 0u; rank[i] = c; }
-}
-
 // One digit-histogram pass.  Each wave takes UT consecutive tokens at a time,
 // with all UT loads issued before the first use (addresses clamped into the
 // matrix).  FIRST: the input is the logits and the key of every score is
@@ -107,7 +101,7 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
     const bool ve = e < E;
     const int ec = min(e, E - 1);
     const uint32_t hmask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
-    const uint32_t pre = prefix[ec] & hmask;
+    const uint32_t pre = (shift == 24) ? 0u : (prefix[ec] & hmask);
     const int64_t t0 = (int64_t)blockIdx.x * tokens_per_block;
     const int64_t t1 = min((int64_t)T, t0 + tokens_per_block);
     for (int64_t tb = t0 + (int64_t)wave * UT; tb < t1; tb += (int64_t)kHistWaves * UT) {
@@ -147,7 +141,7 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
 // top to the one holding the rank-th largest matching key.
 __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     int E, int shift, int nblocks, const uint32_t* __restrict__ partial, uint32_t* __restrict__ prefix,
-    uint32_t* __restrict__ rank)
+    uint32_t* __restrict__ rank, uint32_t c0, float* __restrict__ thr, float* __restrict__ stat, float m)
 {
     __shared__ uint32_t part[kSelectSplit][256];
     const int e = blockIdx.x;
@@ -179,7 +173,9 @@ __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     }
     const int incl = wave_incl_scan(tot);
     const int excl = incl - tot;
-    const int r = (int)rank[e];
+    // the first pass starts from the empty prefix and rank c0
+    const bool first = shift == 24;
+    const int r = first ? (int)c0 : (int)rank[e];
     if (excl < r && r <= incl) {
         int run = excl;
         int pos = 4 * lane + 3;
@@ -189,21 +185,17 @@ __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
             run += (int)c[i];
         }
         const uint32_t bin = 255u - (uint32_t)pos;
-        prefix[e] = prefix[e] | (bin << shift);
+        const uint32_t p = (first ? 0u : prefix[e]) | (bin << shift);
+        prefix[e] = p;
         rank[e] = (uint32_t)(r - run);
+        if (shift == 0) {
+            // the last pass fixed every bit: p is the statistic; apply the EMA
+            const float st = u2f(p);
+            if (stat) stat[e] = st;
+            const float one_minus_m = 1.0f - m;
+            thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
+        }
     }
-}
-
-__global__ __launch_bounds__(kThrThreads) void thr_finalize_kernel(int E, const uint32_t* __restrict__ prefix,
-                                                                   float* __restrict__ thr,
-                                                                   float* __restrict__ stat, float m)
-{
-    const int e = blockIdx.x * kThrThreads + threadIdx.x;
-    if (e >= E) return;
-    const float st = u2f(prefix[e]);
-    if (stat) stat[e] = st;
-    const float one_minus_m = 1.0f - m;
-    thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
 }
 
 }  // namespace et
@@ -245,8 +237,6 @@ extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, i
     const int Ti = (int)T, Ei = (int)E;
     const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
 
-    thr_init_kernel<<<dim3((Ei + kThrThreads - 1) / kThrThreads), dim3(kThrThreads), 0, s>>>(Ei, (uint32_t)c, ws.prefix, ws.rank);
-    if (int rc = check_launch("thr_init_kernel")) return rc;
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
         const HistGrid& g = pass == 0 ? ws.g1 : ws.g2;
@@ -259,9 +249,9 @@ extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, i
                 logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial);
         if (int rc = check_launch("thr_hist_kernel")) return rc;
         thr_select_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(Ei, shift, (int)g.blocks, ws.partial,
-                                                                   ws.prefix, ws.rank);
+                                                                   ws.prefix, ws.rank, (uint32_t)c, thr, stat,
+                                                                   momentum);
         if (int rc = check_launch("thr_select_kernel")) return rc;
     }
-    thr_finalize_kernel<<<dim3((Ei + kThrThreads - 1) / kThrThreads), dim3(kThrThreads), 0, s>>>(Ei, ws.prefix, thr, stat, momentum);
-    return check_launch("thr_finalize_kernel");
+    return ET_OK;
 }
