@@ -84,16 +84,16 @@ __device__ __forceinline__ float exp_nonpos(float x)
 }
 
 // sigmoid(l): l >= 0 -> 1/(1+exp(-l)); l < 0 -> exp(l)/(1+exp(l)); NaN stays NaN.
-// Both divisions are IEEE correctly rounded (HIP's default for binary32).
+// Both cases share z = exp(-|l|) and one division, (l >= 0 ? 1 : z) / (1 + z),
+// so a wave whose lanes straddle 0 evaluates one exp and one division rather
+// than both sides of a branch; the bits are those of the two-case form.  The
+// division is IEEE correctly rounded (HIP's default for binary32).
 __device__ __forceinline__ float sigmoid(float l)
 {
-    if (l != l) return l;
-    if (l >= 0.0f) {
-        float z = exp_nonpos(-l);
-        return 1.0f / (1.0f + z);
-    }
-    float z = exp_nonpos(l);
-    return z / (1.0f + z);
+    const float z = exp_nonpos(-__builtin_fabsf(l));
+    const float num = (l >= 0.0f) ? 1.0f : z;
+    const float s = num / (1.0f + z);
+    return (l != l) ? l : s;
 }
 
 // ---------------------------------------------------------------------------
