@@ -90,6 +90,44 @@ def copy_ceiling(dev, stream, nbytes: int = 1 << 30, reps: int = 5) -> dict:
             "frac": round(2 * nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
 
 
+def threshold_dynamics(et, W, dev, stream, workload: str, seed: int) -> dict:
+    """Routing-only loop of a workload whose thresholds follow the EMA (C5):
+    per step, route a fresh logits batch with the current thresholds (fixed
+    slot capacity, no host sync) and apply the EMA update.  Logits are
+    generated on the device beforehand; the step count is the workload's."""
+    import torch
+    cfg = W.CONFIGS[workload]
+    T, E, steps = cfg["T"], cfg["E"], cfg["steps"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 17)
+    logits = [torch.randn(T, E, device=dev, generator=g) for _ in range(steps)]
+    thr = torch.full((E,), cfg["thr0"], dtype=torch.float32, device=dev)
+    cap = T * E
+    rws = torch.empty(et.route_workspace_bytes(T, E), dtype=torch.uint8, device=dev)
+    tws = torch.empty(et.threshold_workspace_bytes(T, E), dtype=torch.uint8, device=dev)
+    stat = torch.empty(E, dtype=torch.float32, device=dev)
+    plan = et.route(logits[0], thr, slot_capacity=cap, workspace=rws)       # warm-up
+    et.threshold_update_(thr.clone(), logits[0], cfg["k_target"], cfg["momentum"], stat=stat, workspace=tws)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    r_ms = u_ms = 0.0
+    torch.cuda.synchronize()
+    slots = []
+    for i in range(steps):
+        ev[0].record(stream)
+        plan = et.route(logits[i], thr, slot_capacity=cap, workspace=rws)
+        ev[1].record(stream)
+        et.threshold_update_(thr, logits[i], cfg["k_target"], cfg["momentum"], stat=stat, workspace=tws)
+        ev[2].record(stream)
+        slots.append(plan.expert_offsets[E:E + 1])
+        torch.cuda.synchronize()
+        r_ms += ev[0].elapsed_time(ev[1])
+        u_ms += ev[1].elapsed_time(ev[2])
+    k = [int(x) / T for x in slots]
+    return {"steps": steps, "T": T, "E": E, "route_ms": round(r_ms / steps, 4),
+            "ema_update_ms": round(u_ms / steps, 4), "mean_k_first_step": round(k[0], 4),
+            "mean_k_last_step": round(k[-1], 4), "k_target": cfg["k_target"]}
+
+
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
     """The CPU restatement (oracle/, single thread) on the first `tokens`
     tokens of the same workload, running the same five operations as one GPU
@@ -243,6 +281,13 @@ def main() -> int:
                 "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": read_traffic(args.workload),
                 "algorithmic_bytes": abytes[dom], "ms": round(stage_ms[dom], 4)}
 
+    dyn = None
+    if cfg["thr"] == "ema":
+        dyn = threshold_dynamics(et, W, dev, stream, args.workload, args.seed)
+        print(f"  threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
+              f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
+              f"{dyn['mean_k_last_step']}", file=sys.stderr)
+
     cpu = None
     if args.cpu_tokens > 0:
         cpu = cpu_baseline(args.workload, args.seed, min(args.cpu_tokens, T))
@@ -269,6 +314,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "copy_ceiling": copy_ref,
+        "threshold_dynamics": dyn,
         "kernels": kernels,
     }
     for name in STAGES:
