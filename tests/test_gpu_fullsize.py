@@ -72,3 +72,23 @@ def test_fullsize_properties(et, orc, dev, name):
         assert bool(((out.double() - ref).abs() <= tol).all()), fn.__name__
         del out, out2, contrib, ref, amass
     torch.cuda.synchronize()
+
+
+def test_threshold_dynamics_c5_full_size(et, orc, dev):
+    """C5 at its real shape (T=131072, E=64): a few routing steps with the EMA
+    update on fresh logits from thr0 = 0.95, routing and thresholds bit-exact
+    with the oracle at every step."""
+    from test_gpu_parity import assert_route_equal, bits
+
+    cfg = W.CONFIGS["C5"]
+    E = cfg["E"]
+    thr_o = np.full(E, cfg["thr0"], np.float32)
+    thr = dev_f32(thr_o, dev)
+    for step in range(3):
+        lg = W.router_logits("C5", seed=2, step=step)
+        L = dev_f32(lg, dev)
+        assert_route_equal(et.route(L, thr), orc.route(lg, thr_o))
+        stat = et.threshold_update_(thr, L, cfg["k_target"], cfg["momentum"])
+        thr_o, stat_o = orc.threshold_update(lg, thr_o, cfg["k_target"], cfg["momentum"])
+        np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+        np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
