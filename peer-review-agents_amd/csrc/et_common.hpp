@@ -123,6 +123,29 @@ __device__ __forceinline__ int wave_sum_int(int v)
     return v;
 }
 
+// DPP move of a float: lane i takes src from the lane CTRL selects; lanes
+// whose source is out of the row, or whose row is not in ROW_MASK, take 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the wave's 64 lanes with DPP moves only (no LDS round trips):
+// pairs, quads, row_shr 4 and 8 leave each 16-lane row's total in its lane 15;
+// row_bcast 15 and 31 then carry row totals up to lane 63.  The order of the
+// additions is fixed, so the result is deterministic.  Returned wave-uniform.
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v += dpp_mov<0xB1>(v);        // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);        // quad_perm [2,3,0,1]
+    v += dpp_mov<0x114>(v);       // row_shr:4
+    v += dpp_mov<0x118>(v);       // row_shr:8
+    v += dpp_mov<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_mov<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kWave - 1));
+}
+
 // Inclusive prefix sum across the wave.
 __device__ __forceinline__ int wave_incl_scan(int v)
 {

@@ -109,10 +109,10 @@ __device__ __forceinline__ int load_slot_block(const int32_t* __restrict__ tok_s
 // Row pieces.  The vector dispatch and combine kernels split every row into
 // pieces of whole 16-byte chunks and give each (token, piece) pair its own
 // wave: consecutive waves take consecutive pieces of one token, then move to
-// the next token.  On gfx950 many short-lived waves that each move 1-4 KiB
-// stream closer to HBM peak than one wave looping over a whole row (measured
-// at d = 4096 bf16: 1 KiB pieces in 128-thread blocks for the scatter, 4 KiB
-// pieces with non-temporal loads and stores for the gathers).
+// the next token.  On gfx950 many short-lived waves that each move 1 KiB per
+// instruction stream closer to HBM peak than one wave looping over a whole row
+// (measured at d = 4096 bf16 for all three kernels: 1 KiB pieces in 128-thread
+// blocks beat 2-8 KiB pieces and 256-1024-thread blocks).
 // ---------------------------------------------------------------------------
 
 struct PieceSpan {
@@ -317,7 +317,7 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
 
 // Vector path, pass 1: one wave per 1 KiB piece of a token's row.
 // For every slot s of the token the wave writes its piece of dYp[s] and the
-// piece's partial dot <dY[t], Yp[s]> (one wave reduction) to
+// piece's partial dot <dY[t], Yp[s]> (one DPP wave reduction) to
 // part[s * npieces + p].  Yp is read once and dYp written once, both
 // non-temporal.  The wave of piece 0 also zero-fills the token's dlogits row;
 // pass 2 then writes the routed entries.
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
                 o[i] = g * df[i];
             }
             if (on) st16_nt(dyp + (int64_t)s * rb + idx * 16, P::pack(o));
-            const float dot = wave_sum(acc);
+            const float dot = wave_sum_dpp(acc);
             if (lane == 0) part[(int64_t)s * npieces + p] = dot;
         }
     }
