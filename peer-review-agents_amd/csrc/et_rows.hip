@@ -226,16 +226,32 @@ __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
         const int my = load_slot_block(tok_slot, jb, sp.j1);
         const int n = min(kWave, sp.j1 - jb);
-        for (int u = 0; u < n; ++u) {
-            const int s = __builtin_amdgcn_readlane(my, u);
-            if (s < 0 || (int64_t)s >= cap) continue;
-            const float g = GATE ? gate[s] : 1.0f;
+        // Walk the valid slots; the load of the next slot's chunk is issued
+        // at the end of the current slot's iteration.  (Issuing it before the
+        // current slot's arithmetic, a two-deep pipeline, measured slower.)
+        int u = 0;
+        int s = -1;
+        v4u w = {0u, 0u, 0u, 0u};
+        for (; u < n; ++u) {
+            s = __builtin_amdgcn_readlane(my, u);
+            if (s >= 0 && (int64_t)s < cap) break;
+        }
+        if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+        while (u < n) {
+            const int cur = s;
+            const v4u wc = w;
+            for (++u; u < n; ++u) {
+                s = __builtin_amdgcn_readlane(my, u);
+                if (s >= 0 && (int64_t)s < cap) break;
+            }
+            const float g = GATE ? gate[cur] : 1.0f;
             if (on) {
                 float f[N];
-                P::unpack(ld16_nt(yp + (int64_t)s * rb + idx * 16), f);
+                P::unpack(wc, f);
 #pragma unroll
                 for (int i = 0; i < N; ++i) acc[i] = __builtin_fmaf(g, f[i], acc[i]);
             }
+            if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
         }
     }
     if (on) st16_nt(y + (int64_t)sp.t * rb + idx * 16, P::pack(acc));
@@ -350,23 +366,35 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
         const int my = load_slot_block(tok_slot, jb, sp.j1);
         const int n = min(kWave, sp.j1 - jb);
-        for (int u = 0; u < n; ++u) {
-            const int s = __builtin_amdgcn_readlane(my, u);
-            if (s < 0 || (int64_t)s >= cap) continue;
-            const float g = gate[s];
-            v4u w = {0u, 0u, 0u, 0u};
-            if (on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+        // slot walk as in combine_fwd_vec
+        int u = 0;
+        int s = -1;
+        v4u w = {0u, 0u, 0u, 0u};
+        for (; u < n; ++u) {
+            s = __builtin_amdgcn_readlane(my, u);
+            if (s >= 0 && (int64_t)s < cap) break;
+        }
+        if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+        while (u < n) {
+            const int cur = s;
+            const v4u wc = w;
+            for (++u; u < n; ++u) {
+                s = __builtin_amdgcn_readlane(my, u);
+                if (s >= 0 && (int64_t)s < cap) break;
+            }
+            const float g = gate[cur];
             float f[N], o[N];
-            P::unpack(w, f);
+            P::unpack(wc, f);
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < N; ++i) {
                 acc = __builtin_fmaf(df[i], f[i], acc);
                 o[i] = g * df[i];
             }
-            if (on) st16_nt(dyp + (int64_t)s * rb + idx * 16, P::pack(o));
+            if (on) st16_nt(dyp + (int64_t)cur * rb + idx * 16, P::pack(o));
             const float dot = wave_sum_dpp(acc);
-            if (lane == 0) part[(int64_t)s * npieces + p] = dot;
+            if (lane == 0) part[(int64_t)cur * npieces + p] = dot;
+            if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
         }
     }
 }
