@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 2
+#define ET_ABI_VERSION 3
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -161,6 +161,23 @@ size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int64_t num_experts,
                         int64_t k_target, float momentum, float* stat,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Largest expert count of the router GEMM (all experts of a token tile are
+ * accumulated in registers). */
+#define ET_MAX_ROUTER_EXPERTS 256
+
+/*
+ * Router logits (the producer of et_route's input):
+ *   logits[t, e] = sum_k x[t, k] * w[e, k]        (f32 out, binary32 accumulate)
+ *   x bf16 [T, d], w bf16 [E, d] (the router weight in nn.Linear layout),
+ *   16-byte aligned; d a multiple of 8 below 2^22; 1 <= E <= ET_MAX_ROUTER_EXPERTS.
+ * Products of bf16 values are exact in binary32; the sum over k runs in a
+ * fixed order, so repeated calls give identical bits, and integer-valued
+ * inputs whose partial sums stay below 2^24 give the exact integer result.
+ * Implements the router producer that feeds the path (no reference counterpart).
+ */
+int et_router_logits(const void* x, const void* w, int64_t num_tokens, int64_t d, int64_t num_experts,
+                     float* logits, void* stream);
 
 #ifdef __cplusplus
 }

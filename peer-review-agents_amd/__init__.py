@@ -17,6 +17,7 @@ from .expert_threshold import (  # noqa: F401
     dispatch_backward,
     route,
     route_workspace_bytes,
+    router_logits,
     threshold_update_,
     threshold_workspace_bytes,
 )

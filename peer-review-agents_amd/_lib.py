@@ -21,6 +21,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "etmoe.h")
 ET_DTYPE_F32 = 0
 ET_DTYPE_BF16 = 1
 ET_MAX_EXPERTS = 1024
+ET_MAX_ROUTER_EXPERTS = 256
 
 
 class ETMoEError(RuntimeError):
@@ -51,6 +52,7 @@ _SIGNATURES = {
     "et_dispatch_bwd": (_int, [_p, _p, _p, _i64, _i64, _int, _i64, _p, _p]),
     "et_threshold_workspace_bytes": (_sz, [_i64, _i64]),
     "et_threshold_update": (_int, [_p, _p, _i64, _i64, _i64, _f, _p, _p, _sz, _p]),
+    "et_router_logits": (_int, [_p, _p, _i64, _i64, _i64, _p, _p]),
 }
 
 _lib = None

@@ -28,7 +28,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import ET_DTYPE_BF16, ET_DTYPE_F32, ET_MAX_EXPERTS, check, lib
+from ._lib import ET_DTYPE_BF16, ET_DTYPE_F32, ET_MAX_EXPERTS, ET_MAX_ROUTER_EXPERTS, check, lib
 
 _ACT_DTYPES = {torch.float32: ET_DTYPE_F32, torch.bfloat16: ET_DTYPE_BF16}
 
@@ -326,6 +326,36 @@ def threshold_update_(thr: torch.Tensor, logits: torch.Tensor, k_target: int,
                                        _vp(stat), _vp(workspace), wsb, _stream(dev))
     check("et_threshold_update", rc)
     return stat
+
+
+# --------------------------------------------------------------------------- #
+# router producer
+# --------------------------------------------------------------------------- #
+
+def router_logits(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Router logits L = X W^T in float32 from bf16 X [T, d] and W [E, d].
+
+    W is the router weight in nn.Linear layout.  Binary32 accumulation in a
+    fixed order on the matrix cores: repeated calls give identical bits.
+    """
+    _require(x, "x", torch.bfloat16, 2)
+    dev = x.device
+    _require(w, "w", torch.bfloat16, 2, dev)
+    T, d = x.shape
+    E, dw = w.shape
+    if dw != d:
+        raise ValueError(f"w has row length {dw}, x has {d}")
+    if not 1 <= E <= ET_MAX_ROUTER_EXPERTS:
+        raise ValueError(f"num_experts must be in [1, {ET_MAX_ROUTER_EXPERTS}], got {E}")
+    if d < 8 or d % 8 or d >= 1 << 22:
+        raise ValueError(f"d must be a positive multiple of 8 below 2^22, got {d}")
+    if x.data_ptr() % 16 or w.data_ptr() % 16:
+        raise ValueError("x and w must be 16-byte aligned")
+    L = _out_or_new(out, (T, E), torch.float32, dev, "out")
+    with torch.cuda.device(dev):
+        rc = lib().et_router_logits(_vp(x), _vp(w), T, d, E, _vp(L), _stream(dev))
+    check("et_router_logits", rc)
+    return L
 
 
 # --------------------------------------------------------------------------- #

@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 11
+    assert len(syms) == 12
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name
@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 2" in hdr
-    assert et.lib().et_abi_version() == 2
+    assert "#define ET_ABI_VERSION 3" in hdr
+    assert et.lib().et_abi_version() == 3
 
 
 def test_workspace_sizes(et):
@@ -112,3 +112,19 @@ def test_combine_bwd_workspace(et):
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "workspace" in _err(et)
     rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, p, 31, None)
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL
+
+
+def test_router_logits_rejects_bad_arguments(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    assert lib.et_router_logits(p, p, 16, 64, 0, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "num_experts" in _err(et)
+    assert lib.et_router_logits(p, p, 16, 64, 257, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_router_logits(p, p, 16, 12, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "multiple of 8" in _err(et)
+    assert lib.et_router_logits(p, p, -1, 64, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_router_logits(p, None, 16, 64, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_router_logits(ctypes.c_void_p(0x1008), p, 16, 64, 8, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "aligned" in _err(et)
+    assert lib.et_router_logits(p, p, 1 << 25, 64, 128, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_router_logits(p, p, 0, 64, 8, p, None) == 0      # no tokens: nothing to do
