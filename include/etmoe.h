@@ -179,6 +179,27 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
 int et_router_logits(const void* x, const void* w, int64_t num_tokens, int64_t d, int64_t num_experts,
                      float* logits, void* stream);
 
+/* Bytes of device workspace et_router_route needs for T tokens and E experts
+ * (0 if E is outside [1, ET_MAX_ROUTER_EXPERTS]). */
+size_t et_router_route_workspace_bytes(int64_t num_tokens, int64_t num_experts);
+
+/*
+ * Fused router producer + routing: the router GEMM of et_router_logits with the
+ * selection of et_route applied to the logits in registers, so the [T, E]
+ * score matrix is never written (only the routed pairs' gates pass through
+ * the workspace).  All outputs are bit-identical to
+ *     et_router_logits(x, w) -> logits;  et_route(logits, thr, ...)
+ * with the same slot_capacity.  `logits` (f32 [T, E]) may be NULL; if given,
+ * the logits are written as well (for an EMA threshold update on this batch).
+ * Arguments as et_router_logits and et_route.
+ * Implements the router producer fused with the routing step (no reference
+ * counterpart).
+ */
+int et_router_route(const void* x, const void* w, const float* thr, int64_t num_tokens, int64_t d,
+                    int64_t num_experts, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                    int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
+                    float* logits, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,8 @@ from .expert_threshold import (  # noqa: F401
     route,
     route_workspace_bytes,
     router_logits,
+    router_route,
+    router_route_workspace_bytes,
     threshold_update_,
     threshold_workspace_bytes,
 )

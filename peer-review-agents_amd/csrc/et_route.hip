@@ -23,6 +23,7 @@
 #include <algorithm>
 
 #include "et_common.hpp"
+#include "et_route_internal.hpp"
 
 namespace et {
 
@@ -83,19 +84,6 @@ static RouteWs route_ws_layout(void* base, const RoutePlan& p, int64_t E)
     return ws;
 }
 
-// Thresholds of the lane's experts e = 64 g + lane; NaN past E, so that lane
-// never selects.
-template <int GM>
-__device__ __forceinline__ void load_thresholds(const float* __restrict__ thr, int E, int G, float (&th)[GM])
-{
-    const int lane = lane_id();
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        const int e = g * kWave + lane;
-        th[g] = (g < G && e < E) ? thr[e] : __builtin_nanf("");
-    }
-}
-
 // Logits of UT consecutive tokens starting at tb < t1 (NaN past t1 or past
 // E).  Addresses are clamped into the matrix so that every load is issued
 // unconditionally, all before the first use; a guarded load would complete
@@ -123,46 +111,6 @@ __device__ __forceinline__ void load_logits(const float* __restrict__ logits, in
         for (int u = 0; u < UT; ++u)
             if (e >= E || tb + u >= t1) lg[u][g] = __builtin_nanf("");
     }
-}
-
-// Selection of one token: m[g] = ballot(score >= thr) over group g, sc[g] =
-// the lane's score.  A token with no expert gets the argmax expert (NaN lowest,
-// ties to the lowest expert index; lanes past E hold NaN, so an all-NaN token
-// goes to expert 0).  Returns the token's expert count (wave-uniform).
-template <int GM>
-__device__ __forceinline__ int select_token(const float (&lg)[GM], const float (&th)[GM], int G,
-                                            uint64_t (&m)[GM], float (&sc)[GM])
-{
-    const int lane = lane_id();
-    int k = 0;
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        sc[g] = sigmoid(lg[g]);
-        m[g] = (g < G) ? (uint64_t)__ballot(sc[g] >= th[g]) : 0ull;
-        k += (int)__popcll(m[g]);
-    }
-    if (k == 0) {
-        float bv = (sc[0] != sc[0]) ? -1.0f : sc[0];
-        int be = lane;
-#pragma unroll
-        for (int g = 1; g < GM; ++g) {
-            if (g < G) {
-                const float v = (sc[g] != sc[g]) ? -1.0f : sc[g];
-                if (v > bv) { bv = v; be = g * kWave + lane; }
-            }
-        }
-#pragma unroll
-        for (int off = kWave / 2; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, kWave);
-            const int oe = __shfl_xor(be, off, kWave);
-            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
-        }
-        be = __builtin_amdgcn_readfirstlane(be);
-#pragma unroll
-        for (int g = 0; g < GM; ++g) m[g] = (g == (be >> 6)) ? (1ull << (be & (kWave - 1))) : 0ull;
-        k = 1;
-    }
-    return k;
 }
 
 template <int GM, int UT>
@@ -394,6 +342,115 @@ __global__ __launch_bounds__(kRouteThreads) void route_fill_kernel(
     }
 }
 
+// Fill from selection masks (the fused router producer's output): the same
+// slot assignment as route_fill_kernel, with each token's selection read from
+// its mask words instead of recomputed from logits, and each routed pair's
+// gate read from the producer's gate list of its 16-token route group.  Block
+// b = producer tile b, wave i = route group q = b * gpt + i.
+constexpr int kMaxGroupsPerTile = 16;
+
+template <int GM, int UT>
+__global__ __launch_bounds__(kMaxGroupsPerTile * kWave) void route_fill_masks_kernel(
+    const uint32_t* __restrict__ masks, const float* __restrict__ gate_ws, int T, int E, int gpt,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ group_counts,
+    const int32_t* __restrict__ block_base, const int32_t* __restrict__ group_slots,
+    const int32_t* __restrict__ block_slot_base, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ token_offsets, int32_t* __restrict__ sorted_token, float* __restrict__ slot_gate,
+    int32_t* __restrict__ token_slot, int64_t cap)
+{
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int b = (int)blockIdx.x;
+    const int q = b * gpt + wave;
+    const int q0 = b * gpt;
+    const int G = (E + kWave - 1) / kWave;
+    const int nwords = (E + 31) / 32;
+
+    int pos[GM];
+    int run = 0;
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+        const int e = g * kWave + lane;
+        const bool ve = g < G && e < E;
+        const int c = ve ? counts[e] : 0;
+        const int incl = wave_incl_scan(c);
+        const int eo = run + incl - c;
+        run += __builtin_amdgcn_readlane(incl, kWave - 1);
+        // counts of the earlier groups of this tile (all loads issued first)
+        const int ec = min(e, E - 1);
+        int prev[kMaxGroupsPerTile - 1];
+#pragma unroll
+        for (int i = 0; i < kMaxGroupsPerTile - 1; ++i) prev[i] = group_counts[(int64_t)min(q0 + i, q) * E + ec];
+        int base = eo + block_base[(int64_t)b * E + ec];
+#pragma unroll
+        for (int i = 0; i < kMaxGroupsPerTile - 1; ++i) base += (i < wave) ? prev[i] : 0;
+        pos[g] = ve ? base : 0;
+        if (ve && q == 0) expert_offsets[e] = eo;
+    }
+    if (q == 0 && lane == 0) {
+        expert_offsets[E] = run;
+        token_offsets[T] = run;
+    }
+    int tok_pos = block_slot_base[b];
+    {
+        int prev[kMaxGroupsPerTile - 1];
+#pragma unroll
+        for (int i = 0; i < kMaxGroupsPerTile - 1; ++i) prev[i] = group_slots[min(q0 + i, q)];
+#pragma unroll
+        for (int i = 0; i < kMaxGroupsPerTile - 1; ++i) tok_pos += (i < wave) ? prev[i] : 0;
+    }
+    const int tok_pos0 = tok_pos;
+    const float* gl = gate_ws + (int64_t)q * 16 * E;
+
+    const int64_t t0 = (int64_t)q * 16;
+    const int64_t t1 = std::min<int64_t>(T, t0 + 16);
+    for (int64_t tb = t0; tb < t1; tb += UT) {
+        // mask word of the lane's expert in each group, for UT tokens (clamped
+        // loads, all issued before the first use)
+        uint32_t wv[UT][GM];
+#pragma unroll
+        for (int g = 0; g < GM; ++g) {
+            const int wi = min(2 * g + (lane >> 5), nwords - 1);
+#pragma unroll
+            for (int u = 0; u < UT; ++u) wv[u][g] = masks[min(tb + u, t1 - 1) * nwords + wi];
+        }
+#pragma unroll
+        for (int u = 0; u < UT; ++u) {
+            if (tb + u >= t1) break;
+            const int t = (int)(tb + u);
+            uint64_t m[GM];
+            int k = 0;
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                const int e = g * kWave + lane;
+                const bool bit = g < G && e < E && ((wv[u][g] >> (lane & 31)) & 1u);
+                m[g] = (uint64_t)__ballot(bit);
+                k += (int)__popcll(m[g]);
+            }
+            if (lane == 0) token_offsets[t] = tok_pos;
+            int below = 0;
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                if (g < G) {
+                    if ((m[g] >> lane) & 1ull) {
+                        const int rank = below + rank_below(m[g]);
+                        const int gi = min(tok_pos - tok_pos0 + rank, 16 * E - 1);   // within the group's list
+                        const float gate = gl[gi];
+                        if ((int64_t)pos[g] < cap) {
+                            sorted_token[pos[g]] = t;
+                            slot_gate[pos[g]] = gate;
+                        }
+                        if ((int64_t)tok_pos + rank < cap) token_slot[tok_pos + rank] = pos[g];
+                        ++pos[g];
+                    }
+                    below += (int)__popcll(m[g]);
+                }
+            }
+            tok_pos += k;
+        }
+    }
+}
+
 // Expert-group bucket (GM) and tokens in flight per wave (UT = 32 / GM keeps
 // the logits of UT tokens x GM groups in 32 VGPRs).
 #define ET_SWITCH_GROUPS(G, ...)                                                            \
@@ -402,6 +459,36 @@ __global__ __launch_bounds__(kRouteThreads) void route_fill_kernel(
     else if ((G) <= 4) { constexpr int GM = 4, UT = 8; __VA_ARGS__; }                      \
     else if ((G) <= 8) { constexpr int GM = 8, UT = 4; __VA_ARGS__; }                      \
     else { constexpr int GM = 16, UT = 2; __VA_ARGS__; }
+
+}  // namespace et
+
+namespace et {
+
+int launch_route_scan(const int32_t* block_counts, const int32_t* block_slots, int NB, int E, int32_t* counts,
+                      int32_t* block_base, int32_t* block_slot_base, hipStream_t s)
+{
+    const int G = (E + kWave - 1) / kWave;
+    route_scan_kernel<<<dim3(G + 1), dim3(kScanThreads), 0, s>>>(block_counts, block_slots, NB, E, counts, block_base,
+                                                                  block_slot_base);
+    return check_launch("route_scan_kernel");
+}
+
+int launch_route_fill_masks(const uint32_t* masks, const float* gate_ws, int T, int E, int gpt, int NB,
+                            const int32_t* counts, const int32_t* group_counts, const int32_t* block_base,
+                            const int32_t* group_slots, const int32_t* block_slot_base, int32_t* expert_offsets,
+                            int32_t* token_offsets, int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                            int64_t cap, hipStream_t s)
+{
+    if (gpt < 1 || gpt > kMaxGroupsPerTile)
+        return fail(ET_ERR_INVALID_ARGUMENT, "route_fill_masks: route groups per tile must be 1..16");
+    if (NB == 0) return ET_OK;
+    const int G = (E + kWave - 1) / kWave;
+    ET_SWITCH_GROUPS(G, route_fill_masks_kernel<GM, UT><<<dim3(NB), dim3(gpt * kWave), 0, s>>>(
+                            masks, gate_ws, T, E, gpt, counts, group_counts, block_base, group_slots,
+                            block_slot_base, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
+                            cap));
+    return check_launch("route_fill_masks_kernel");
+}
 
 }  // namespace et
 

@@ -1,0 +1,95 @@
+// et_route_internal.hpp -- the selection rule (device) and the host-side
+// launchers of the routing kernels shared by the logit-input routing
+// (et_route.hip) and the fused router producer (et_router.hip).  Not part of
+// the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "et_common.hpp"
+
+namespace et {
+
+// ---------------------------------------------------------------------------
+// the selection rule, shared by every routing kernel (device)
+// ---------------------------------------------------------------------------
+
+// Thresholds of the lane's experts e = 64 g + lane; NaN past E, so that lane
+// never selects.
+template <int GM>
+__device__ __forceinline__ void load_thresholds(const float* __restrict__ thr, int E, int G, float (&th)[GM])
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+        const int e = g * kWave + lane;
+        th[g] = (g < G && e < E) ? thr[e] : __builtin_nanf("");
+    }
+}
+
+// Selection of one token: m[g] = ballot(score >= thr) over group g, sc[g] =
+// the lane's score.  A token with no expert gets the argmax expert (NaN lowest,
+// ties to the lowest expert index; lanes past E hold NaN, so an all-NaN token
+// goes to expert 0).  Returns the token's expert count (wave-uniform).
+template <int GM>
+__device__ __forceinline__ int select_token(const float (&lg)[GM], const float (&th)[GM], int G,
+                                            uint64_t (&m)[GM], float (&sc)[GM])
+{
+    const int lane = lane_id();
+    int k = 0;
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+        sc[g] = sigmoid(lg[g]);
+        m[g] = (g < G) ? (uint64_t)__ballot(sc[g] >= th[g]) : 0ull;
+        k += (int)__popcll(m[g]);
+    }
+    if (k == 0) {
+        float bv = (sc[0] != sc[0]) ? -1.0f : sc[0];
+        int be = lane;
+#pragma unroll
+        for (int g = 1; g < GM; ++g) {
+            if (g < G) {
+                const float v = (sc[g] != sc[g]) ? -1.0f : sc[g];
+                if (v > bv) { bv = v; be = g * kWave + lane; }
+            }
+        }
+#pragma unroll
+        for (int off = kWave / 2; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, kWave);
+            const int oe = __shfl_xor(be, off, kWave);
+            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+        }
+        be = __builtin_amdgcn_readfirstlane(be);
+#pragma unroll
+        for (int g = 0; g < GM; ++g) m[g] = (g == (be >> 6)) ? (1ull << (be & (kWave - 1))) : 0ull;
+        k = 1;
+    }
+    return k;
+}
+
+// ---------------------------------------------------------------------------
+// host-side launchers
+// ---------------------------------------------------------------------------
+
+// Column-wise exclusive scan of the per-block expert counts (NB rows of E)
+// into counts[E] and block_base[NB * E], and of the per-block slot totals
+// into block_slot_base[NB].
+int launch_route_scan(const int32_t* block_counts, const int32_t* block_slots, int NB, int E, int32_t* counts,
+                      int32_t* block_base, int32_t* block_slot_base, hipStream_t s);
+
+// Routing outputs from per-token selection masks.  Tokens are split into
+// route groups of 16 (group q = tokens [16 q, 16 q + 16)), gpt groups per
+// block tile (NB tiles).  Token t's selection is masks[t * nwords + e / 32]
+// bit e % 32 (nwords = ceil(E / 32)); group q's routed gates are stored in
+// token order, ascending expert within a token, from gate_ws[q * 16 * E].
+// group_counts / group_slots are the producer's per-group expert counts and
+// slot totals; counts, block_base and block_slot_base come from
+// launch_route_scan over the tiles.
+int launch_route_fill_masks(const uint32_t* masks, const float* gate_ws, int T, int E, int gpt, int NB,
+                            const int32_t* counts, const int32_t* group_counts, const int32_t* block_base,
+                            const int32_t* group_slots, const int32_t* block_slot_base, int32_t* expert_offsets,
+                            int32_t* token_offsets, int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                            int64_t cap, hipStream_t s);
+
+}  // namespace et

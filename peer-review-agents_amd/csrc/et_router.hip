@@ -18,6 +18,7 @@
 #include <algorithm>
 
 #include "et_common.hpp"
+#include "et_route_internal.hpp"
 
 namespace et {
 
@@ -48,17 +49,144 @@ template <int NT, int MW, int MT, int R> struct RtShape {
     static_assert(R % 2 == 0, "the W register double buffer is indexed by ring position");
 };
 
+// Outputs of the routing epilogue (ROUTE = true), by 16-token route group
+// (group q = tokens [16 q, 16 q + 16)) and by block tile.
+struct RouteEpilogue {
+    const float* thr;          // [E]
+    uint32_t* masks;           // [T * nwords], nwords = ceil(E / 32): token t's selection, bit e % 32 of word e / 32
+    float* gate_ws;            // [ngroups * 16 * E]: group q's routed gates in token order, ascending expert
+    int32_t* group_counts;     // [ngroups * E]
+    int32_t* block_counts;     // [ntiles * E]
+    int32_t* group_slots;      // [ngroups]
+    int32_t* block_slots;      // [ntiles]
+};
+
+// Routing epilogue of one producer tile.  The wave's logits pass through a
+// wave-private LDS buffer, 16 tokens at a time, and are then walked token by
+// token with lane = expert, through the same select_token as et_route (so the
+// selection, gates and argmax fallback are those of et_route by construction).
+// acc[m][n][j] is the logit of token t0 + 32 m + r, r = 8 (j / 4) +
+// 4 (lane / 32) + j % 4, expert 32 n + lane % 32.  Ends with a barrier.
+template <int NT, int MW, int MT>
+__device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], const RouteEpilogue& ro,
+                                               float* rbuf, int* red, int tile, int wave, int64_t t0, int T, int E)
+{
+    constexpr int P = NT * 32 + 8;              // LDS row pitch (floats): both halves' writes on distinct banks
+    constexpr int GM = (NT * 32 + kWave - 1) / kWave;
+    const int lane = lane_id();
+    const int half = lane >> 5;
+    const int row = lane & 31;
+    const int G = (E + kWave - 1) / kWave;
+    const int nwords = (E + 31) / 32;
+    float th[GM];
+    load_thresholds<GM>(ro.thr, E, G, th);
+    int wcnt[GM];
+#pragma unroll
+    for (int g = 0; g < GM; ++g) wcnt[g] = 0;
+    int wslots = 0;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            // tokens 16 hh .. 16 hh + 15 of token tile m <- j = 8 hh .. 8 hh + 7
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int j = 8 * hh + jj;
+                    const int u = 8 * (jj / 4) + 4 * half + (j % 4);
+                    rbuf[u * P + n * 32 + row] = acc[m][n][j];
+                }
+            __syncthreads();
+            const int64_t tg = t0 + m * 32 + 16 * hh;     // first token of the route group
+            const int64_t q = tg / 16;
+            float* gl = ro.gate_ws + q * 16 * (int64_t)E;
+            int cnt[GM];
+#pragma unroll
+            for (int g = 0; g < GM; ++g) cnt[g] = 0;
+            int lp = 0;
+            const int nu = (int)std::min<int64_t>(16, std::max<int64_t>(0, (int64_t)T - tg));
+#pragma unroll 4
+            for (int u = 0; u < nu; ++u) {
+                const int64_t t = tg + u;
+                float lg[GM];
+#pragma unroll
+                for (int g = 0; g < GM; ++g) {
+                    const int e = g * kWave + lane;
+                    lg[g] = (g < G && e < E) ? rbuf[u * P + e] : __builtin_nanf("");
+                }
+                uint64_t mm[GM];
+                float sc[GM];
+                const int k = select_token<GM>(lg, th, G, mm, sc);
+                uint32_t word = 0u;                     // lane i < nwords writes mask word i
+#pragma unroll
+                for (int g = 0; g < GM; ++g) {
+                    if (lane == 2 * g) word = (uint32_t)mm[g];
+                    if (lane == 2 * g + 1) word = (uint32_t)(mm[g] >> 32);
+                }
+                if (lane < nwords) ro.masks[t * nwords + lane] = word;
+                int below = 0;
+#pragma unroll
+                for (int g = 0; g < GM; ++g) {
+                    if (g < G) {
+                        if ((mm[g] >> lane) & 1ull) {
+                            const int gi = lp + below + rank_below(mm[g]);
+                            if (gi < 16 * E) gl[gi] = sc[g];
+                            ++cnt[g];
+                        }
+                        below += (int)__popcll(mm[g]);
+                    }
+                }
+                lp += k;
+            }
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                const int e = g * kWave + lane;
+                if (g < G && e < E) ro.group_counts[q * E + e] = cnt[g];
+                wcnt[g] += cnt[g];
+            }
+            if (lane == 0) ro.group_slots[q] = lp;
+            wslots += lp;
+            __syncthreads();                            // rbuf is rewritten by the next group
+        }
+    }
+    // tile sums through LDS
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+        const int e = g * kWave + lane;
+        if (g < G && e < E) red[wave * E + e] = wcnt[g];
+    }
+    if (lane == 0) red[MW * E + wave] = wslots;
+    __syncthreads();
+    for (int e = (int)threadIdx.x; e < E; e += MW * kWave) {
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < MW; ++i) sum += red[i * E + e];
+        ro.block_counts[(int64_t)tile * E + e] = sum;
+    }
+    if (threadIdx.x == 0) {
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < MW; ++i) sum += red[MW * E + i];
+        ro.block_slots[tile] = sum;
+    }
+    __syncthreads();
+}
+
 // A block owns TOK tokens at a time and loops over token tiles (the grid is
 // capped); wave w owns tokens [t0, t0 + 32 * MT).  Every wave sums k in
 // ascending k-steps of 16, one MFMA per step, token tile and expert tile, so
 // the bits of a logit depend on d only -- not on T, E or the tiling.
-template <int NT, int MW, int MT, int R>
+template <int NT, int MW, int MT, int R, bool ROUTE>
 __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int d, int E,
-    float* __restrict__ logits)
+    float* __restrict__ logits, RouteEpilogue ro)
 {
     using S = RtShape<NT, MW, MT, R>;
+    static_assert(!ROUTE || MW * NT * 32 + MW <= NT * 32 * S::PITCH, "epilogue reduction must fit the W buffer");
     __shared__ uint16_t wl[2][NT * 32 * S::PITCH];
+    // routing epilogue: 16 tokens x (NT * 32 + 8) floats per wave
+    __shared__ float rbuf[ROUTE ? MW * 16 * (NT * 32 + 8) : 1];
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -173,30 +301,35 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             if (nmain + r < nchunks) step(nmain + r, r);
 
         // epilogue: lane l writes expert n * 32 + l % 32 of 16 token rows per tile
+        if (!ROUTE || logits != nullptr) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+            for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                const int e = n * 32 + row;
+                for (int n = 0; n < NT; ++n) {
+                    const int e = n * 32 + row;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int64_t t = t0 + m * 32 + 8 * (j / 4) + 4 * half + (j % 4);
-                    if (t < T && e < E) logits[t * E + e] = acc[m][n][j];
+                    for (int j = 0; j < 16; ++j) {
+                        const int64_t t = t0 + m * 32 + 8 * (j / 4) + 4 * half + (j % 4);
+                        if (t < T && e < E) logits[t * E + e] = acc[m][n][j];
+                    }
                 }
-            }
+        }
+        if constexpr (ROUTE)
+            route_epilogue<NT, MW, MT>(acc, ro, rbuf + wave * 16 * (NT * 32 + 8), reinterpret_cast<int*>(wl[0]), tile,
+                                       wave, t0, T, E);
     }
 }
 
 // X ring length: 12-16 KiB of X in flight per wave.
 template <int NT, int MT> constexpr int kRouterRing = (NT <= 4 ? 4 : 8) / MT;
 
-template <int NT, int MW, int MT>
+template <int NT, int MW, int MT, bool ROUTE>
 static void launch_router(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* w, int64_t T, int64_t d,
-                          int64_t E, float* logits)
+                          int64_t E, float* logits, const RouteEpilogue& ro)
 {
     constexpr int MTE = NT == 8 ? 1 : MT;       // two token tiles of 8 expert tiles do not fit the registers
-    router_logits_kernel<NT, MW, MTE, kRouterRing<NT, MTE>>
-        <<<grid, dim3(MW * kWave), 0, s>>>(x, w, (int)T, (int)d, (int)E, logits);
+    router_logits_kernel<NT, MW, MTE, kRouterRing<NT, MTE>, ROUTE>
+        <<<grid, dim3(MW * kWave), 0, s>>>(x, w, (int)T, (int)d, (int)E, logits, ro);
 }
 
 // Launch shape by batch size: the largest token tile that still gives every
@@ -209,11 +342,13 @@ struct RouterLaunch {
 };
 constexpr int64_t kRouterMaxBlocks = 2048;
 
-static RouterLaunch router_launch(int64_t T)
+static RouterLaunch router_launch(int64_t T, int nt)
 {
-    if (T >= 256 * 256) return {4, 2};
-    if (T >= 256 * 128) return {2, 2};
-    return {2, 1};
+    RouterLaunch L{2, 1};
+    if (T >= 256 * 256) L = {4, 2};
+    else if (T >= 256 * 128) L = {2, 2};
+    if (nt > 4) L.mt = 1;
+    return L;
 }
 
 #define ET_SWITCH_NT(nt, ...)                                                   \
@@ -257,12 +392,113 @@ extern "C" int et_router_logits(const void* x, const void* w, int64_t T, int64_t
         return fail(ET_ERR_INVALID_ARGUMENT, "et_router_logits: x and w must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int nt = (int)((E + 31) / 32);
-    const RouterLaunch L = router_launch(T);
-    const int mt = nt == 8 ? 1 : L.mt;
-    const int64_t ntiles = (T + 32 * L.mw * mt - 1) / (32 * L.mw * mt);
+    const RouterLaunch L = router_launch(T, nt);
+    const int64_t ntiles = (T + 32 * L.mw * L.mt - 1) / (32 * L.mw * L.mt);
     const dim3 grid((unsigned)std::min<int64_t>(ntiles, kRouterMaxBlocks));
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint16_t* wp = static_cast<const uint16_t*>(w);
-    ET_SWITCH_NT(nt, ET_SWITCH_MW(L.mw, ET_SWITCH_MT(L.mt, launch_router<NT, MW, MT>(grid, s, xp, wp, T, d, E, logits))));
+    ET_SWITCH_NT(nt, ET_SWITCH_MW(L.mw, ET_SWITCH_MT(L.mt, launch_router<NT, MW, MT, false>(
+                                                               grid, s, xp, wp, T, d, E, logits, RouteEpilogue{}))));
     return check_launch("router_logits_kernel");
+}
+
+namespace {
+
+// Workspace of et_router_route: the tokens split into block tiles of
+// 32 * mw * mt tokens and route groups of 16.
+struct RouterRouteWs {
+    uint32_t* masks;           // [T * nwords]
+    float* gate_ws;            // [ngroups * 16 * E]
+    int32_t* group_counts;     // [ngroups * E]
+    int32_t* block_counts;     // [ntiles * E]
+    int32_t* block_base;       // [ntiles * E]
+    int32_t* group_slots;      // [ngroups]
+    int32_t* block_slots;      // [ntiles]
+    int32_t* block_slot_base;  // [ntiles]
+    int64_t ntiles, gpt;
+    size_t bytes;
+};
+
+RouterRouteWs router_route_ws(void* base, int64_t T, int64_t E, const RouterLaunch& L)
+{
+    const int64_t tok = 32 * L.mw * L.mt;
+    RouterRouteWs ws{};
+    ws.ntiles = (T + tok - 1) / tok;
+    ws.gpt = tok / 16;
+    const int64_t ngroups = ws.ntiles * ws.gpt;
+    const int64_t nwords = (E + 31) / 32;
+    size_t off = 0;
+    char* b = static_cast<char*>(base);
+    auto take = [&](int64_t n) {
+        void* q = b + off;
+        off += (size_t(n) * 4 + 255) & ~size_t(255);
+        return q;
+    };
+    ws.masks = static_cast<uint32_t*>(take(T * nwords));
+    ws.gate_ws = static_cast<float*>(take(ngroups * 16 * E));
+    ws.group_counts = static_cast<int32_t*>(take(ngroups * E));
+    ws.block_counts = static_cast<int32_t*>(take(ws.ntiles * E));
+    ws.block_base = static_cast<int32_t*>(take(ws.ntiles * E));
+    ws.group_slots = static_cast<int32_t*>(take(ngroups));
+    ws.block_slots = static_cast<int32_t*>(take(ws.ntiles));
+    ws.block_slot_base = static_cast<int32_t*>(take(ws.ntiles));
+    ws.bytes = off;
+    return ws;
+}
+
+}  // namespace
+
+extern "C" size_t et_router_route_workspace_bytes(int64_t num_tokens, int64_t num_experts)
+{
+    if (num_tokens < 0 || num_experts < 1 || num_experts > ET_MAX_ROUTER_EXPERTS) return 0;
+    const RouterLaunch L = router_launch(num_tokens, (int)((num_experts + 31) / 32));
+    return router_route_ws(nullptr, num_tokens, num_experts, L).bytes;
+}
+
+extern "C" int et_router_route(const void* x, const void* w, const float* thr, int64_t T, int64_t d, int64_t E,
+                               int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                               int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
+                               float* logits, void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (T < 0 || T >= (int64_t(1) << 31)) return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: num_tokens out of range");
+    if (E < 1 || E > ET_MAX_ROUTER_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_ROUTER_EXPERTS) + "]");
+    if (d < 1 || d % 8 != 0 || d >= (int64_t(1) << 22))
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: d must be a positive multiple of 8 below 2^22");
+    if (T * E >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: num_tokens * num_experts must be < 2^31");
+    if (slot_capacity < 0) return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: slot_capacity < 0");
+    if (!thr || !counts || !expert_offsets || !token_offsets || !workspace)
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: null thr/counts/offsets/workspace pointer");
+    if (T > 0 && (!x || !w)) return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: null x or w");
+    if (slot_capacity > 0 && (!sorted_token || !slot_gate || !token_slot))
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: null slot array with slot_capacity > 0");
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
+        return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: x and w must be 16-byte aligned");
+    const int nt = (int)((E + 31) / 32);
+    const RouterLaunch L = router_launch(T, nt);
+    const RouterRouteWs ws = router_route_ws(workspace, T, E, L);
+    if (workspace_bytes < ws.bytes)
+        return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_router_route: workspace needs " + std::to_string(ws.bytes) +
+                                                    " bytes, got " + std::to_string(workspace_bytes));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t ntiles = ws.ntiles;
+    if (ntiles > 0) {
+        const dim3 grid((unsigned)std::min<int64_t>(ntiles, kRouterMaxBlocks));
+        const RouteEpilogue ro{thr, ws.masks, ws.gate_ws, ws.group_counts, ws.block_counts, ws.group_slots,
+                               ws.block_slots};
+        const uint16_t* xp = static_cast<const uint16_t*>(x);
+        const uint16_t* wp = static_cast<const uint16_t*>(w);
+        ET_SWITCH_NT(nt, ET_SWITCH_MW(L.mw, ET_SWITCH_MT(L.mt, launch_router<NT, MW, MT, true>(
+                                                                   grid, s, xp, wp, T, d, E, logits, ro))));
+        if (int rc = check_launch("router_logits_kernel (route)")) return rc;
+    }
+    if (int rc = launch_route_scan(ws.block_counts, ws.block_slots, (int)ntiles, (int)E, counts, ws.block_base,
+                                   ws.block_slot_base, s))
+        return rc;
+    return launch_route_fill_masks(ws.masks, ws.gate_ws, (int)T, (int)E, (int)ws.gpt, (int)ntiles, counts,
+                                   ws.group_counts, ws.block_base, ws.group_slots, ws.block_slot_base,
+                                   expert_offsets, token_offsets, sorted_token, slot_gate, token_slot, slot_capacity,
+                                   s);
 }

@@ -358,6 +358,71 @@ def router_logits(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] 
     return L
 
 
+def router_route_workspace_bytes(num_tokens: int, num_experts: int) -> int:
+    return int(lib().et_router_route_workspace_bytes(num_tokens, num_experts))
+
+
+def router_route(x: torch.Tensor, w: torch.Tensor, thr: torch.Tensor, *, slot_capacity: Optional[int] = None,
+                 return_logits: bool = False, logits_out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None):
+    """Router GEMM fused with routing: ``route(router_logits(x, w), thr)``
+    without writing the [T, E] scores.  Bit-identical to that composition.
+
+    Returns the RoutingPlan, or (plan, logits) when ``return_logits`` is set or
+    ``logits_out`` is given (the logits are then written too, e.g. for
+    :func:`threshold_update_` on this batch).
+    """
+    _require(x, "x", torch.bfloat16, 2)
+    dev = x.device
+    _require(w, "w", torch.bfloat16, 2, dev)
+    T, d = x.shape
+    E, dw = w.shape
+    if dw != d:
+        raise ValueError(f"w has row length {dw}, x has {d}")
+    if not 1 <= E <= ET_MAX_ROUTER_EXPERTS:
+        raise ValueError(f"num_experts must be in [1, {ET_MAX_ROUTER_EXPERTS}], got {E}")
+    if d < 8 or d % 8 or d >= 1 << 22:
+        raise ValueError(f"d must be a positive multiple of 8 below 2^22, got {d}")
+    if x.data_ptr() % 16 or w.data_ptr() % 16:
+        raise ValueError("x and w must be 16-byte aligned")
+    _require(thr, "thr", torch.float32, 1, dev)
+    if thr.shape[0] != E:
+        raise ValueError(f"thr has {thr.shape[0]} entries, w has {E} experts")
+    if T * E >= 2 ** 31:
+        raise ValueError("num_tokens * num_experts must be < 2^31 (int32 slot indices)")
+    sync = slot_capacity is None
+    cap = T * E if sync else int(slot_capacity)
+    if cap < 0:
+        raise ValueError("slot_capacity must be >= 0")
+    want_logits = return_logits or logits_out is not None
+    L = _out_or_new(logits_out, (T, E), torch.float32, dev, "logits_out") if want_logits else None
+    i32 = dict(dtype=torch.int32, device=dev)
+    counts = torch.empty(E, **i32)
+    eo = torch.empty(E + 1, **i32)
+    to = torch.empty(T + 1, **i32)
+    st = torch.empty(cap, **i32)
+    sg = torch.empty(cap, dtype=torch.float32, device=dev)
+    ts = torch.empty(cap, **i32)
+    wsb = router_route_workspace_bytes(T, E)
+    if workspace is None:
+        workspace = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace must hold {wsb} bytes on {dev}")
+    with torch.cuda.device(dev):
+        rc = lib().et_router_route(_vp(x), _vp(w), _vp(thr), T, d, E, _vp(counts), _vp(eo), _vp(to), _vp(st),
+                                   _vp(sg), _vp(ts), cap, _vp(L), _vp(workspace), wsb, _stream(dev))
+    check("et_router_route", rc)
+    plan = RoutingPlan(counts, eo, to, st, sg, ts, T, E, cap)
+    if sync:
+        S = int(eo[E].item())
+        plan.num_slots = S
+        plan.sorted_token = st[:S]
+        plan.slot_gate = sg[:S]
+        plan.token_slot = ts[:S]
+        plan.capacity = S
+    return (plan, L) if want_logits else plan
+
+
 # --------------------------------------------------------------------------- #
 # autograd wrappers
 # --------------------------------------------------------------------------- #

@@ -117,3 +117,85 @@ def test_router_logits_host_validation(et, dev):
         et.router_logits(base[4:].view(8, 64), torch.zeros(4, 64, device=dev, dtype=bf))
     with pytest.raises(ValueError):
         et.router_logits(x, torch.zeros(4, 64, device=dev, dtype=bf), out=torch.zeros(8, 5, device=dev))
+
+
+# --------------------------------------------------------------------------- #
+# fused producer + routing: bit-identical to router_logits followed by route
+# --------------------------------------------------------------------------- #
+
+def _assert_plans_identical(a, b):
+    for f in ("counts", "expert_offsets", "token_offsets", "sorted_token", "token_slot"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    assert torch.equal(a.slot_gate.view(torch.int32), b.slot_gate.view(torch.int32))
+
+
+def _router_case(dev, T, d, E, seed, q):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn(T, d, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(E, d, generator=g, device=dev) * d ** -0.5).to(torch.bfloat16)
+    return x, w
+
+
+ROUTE_SHAPES = [  # (T, d, E, per-expert threshold quantile)
+    (1, 8, 1, 0.5), (5, 24, 8, 0.75), (130, 520, 40, 0.9), (1000, 256, 128, 0.95), (300, 256, 200, 0.97),
+    (129, 64, 256, 0.99), (33001, 136, 40, 0.8), (66001, 72, 100, 0.93), (70003, 64, 256, 0.97),
+    (16384, 2048, 64, 0.875), (4096, 512, 8, 0.75),
+]
+
+
+@pytest.mark.parametrize("T,d,E,q", ROUTE_SHAPES)
+def test_router_route_matches_composition(et, dev, T, d, E, q):
+    print(f"router_route T={T} d={d} E={E} q={q}", flush=True)
+    x, w = _router_case(dev, T, d, E, T + 17 * E, q)
+    L = et.router_logits(x, w)
+    thr = torch.quantile(torch.sigmoid(L.double()), q, dim=0).float().contiguous()
+    thr[0] = 2.0                                   # expert 0 unreachable by threshold: only argmax fallbacks
+    want = et.route(L, thr)
+    got, L2 = et.router_route(x, w, thr, return_logits=True)
+    assert got.num_slots == want.num_slots
+    _assert_plans_identical(got, want)
+    assert torch.equal(L2.view(torch.int32), L.view(torch.int32))
+    assert et.router_route(x, w, thr).num_slots == want.num_slots      # the scores-free variant
+
+
+def test_router_route_argmax_fallback_and_nonfinite(et, dev):
+    T, d, E = 2000, 128, 96
+    x, w = _router_case(dev, T, d, E, 5, 0.9)
+    x[3, 0] = float("inf")                         # +-inf logits
+    x[4, :16] = float("inf")
+    x[5, 0] = float("inf")
+    x[5, 1] = float("-inf")                        # inf - inf: NaN logits
+    x[6] = float("nan")
+    L = et.router_logits(x, w)
+    assert bool(torch.isnan(L).any()) and bool(torch.isinf(L).any())
+    for thr_val in (0.5, 0.999, 1.5):              # 1.5: every token falls back to its argmax expert
+        thr = torch.full((E,), thr_val, device=dev)
+        _assert_plans_identical(et.router_route(x, w, thr), et.route(L, thr))
+
+
+def test_router_route_explicit_and_undersized_capacity(et, dev):
+    T, d, E = 3000, 256, 64
+    x, w = _router_case(dev, T, d, E, 9, 0.9)
+    L = et.router_logits(x, w)
+    thr = torch.quantile(torch.sigmoid(L.double()), 0.9, dim=0).float().contiguous()
+    S = et.route(L, thr).num_slots
+    for cap in (S, S // 2, 0):
+        a = et.router_route(x, w, thr, slot_capacity=cap)
+        b = et.route(L, thr, slot_capacity=cap)
+        assert a.num_slots is None and a.capacity == cap
+        _assert_plans_identical(a, b)
+
+
+def test_router_route_full_size_c3(et, orc, dev):
+    cfg = W.CONFIGS["C3"]
+    T, d, E = cfg["T"], cfg["d"], cfg["E"]
+    print(f"router_route C3 T={T} d={d} E={E}", flush=True)
+    x, w = _router_case(dev, T, d, E, 31, 0.0)
+    L = et.router_logits(x, w)
+    lg = host(L)
+    thr_h = W.thresholds("C3", lg)
+    thr = torch.from_numpy(thr_h).to(dev)
+    got = et.router_route(x, w, thr)
+    _assert_plans_identical(got, et.route(L, thr))
+    assert_route_equal(got, orc.route(lg, thr_h))
