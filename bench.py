@@ -7,6 +7,8 @@ resident in HBM before timing starts:
     combine_fwd      Y  = sum_s gate[s] * Yp[s]
     combine_bwd      dYp = gate * dY[token], dgate = <dY, Yp>, dlogits (router grad)
     dispatch_bwd     dX = sum_s dXp[s]
+The router producer (router logits GEMM, fused producer + routing) is
+measured separately after the timed steps and reported in "router_producer".
 Yp and dXp are separate resident buffers standing in for the expert FFN's
 output and input-gradient (the FFN itself is not part of the path).
 
@@ -126,6 +128,49 @@ def threshold_dynamics(et, W, dev, stream, workload: str, seed: int) -> dict:
     return {"steps": steps, "T": T, "E": E, "route_ms": round(r_ms / steps, 4),
             "ema_update_ms": round(u_ms / steps, 4), "mean_k_first_step": round(k[0], 4),
             "mean_k_last_step": round(k[-1], 4), "k_target": cfg["k_target"]}
+
+
+def router_producer(et, dev, stream, X, E: int, reps: int = 10) -> dict:
+    """The router producer on the workload's resident activations X (bf16):
+    logits = X W^T (router_logits_kernel), the fused producer + routing
+    (et_router_route, scores never written) against router_logits followed by
+    et_route, and torch's bf16 linear as a library reference.  Measured with
+    HIP events on the stream the kernels run on, outside the timed step."""
+    import torch
+    T, d = X.shape
+    g = torch.Generator(device=dev)
+    g.manual_seed(4242)
+    Wr = (torch.randn(E, d, device=dev, generator=g) * d ** -0.5).to(torch.bfloat16)
+    L = et.router_logits(X, Wr)
+    q = max(0.0, 1.0 - 8.0 / E)
+    thr = torch.quantile(torch.sigmoid(L[:8192].double()), q, dim=0).float().contiguous()
+    cap = et.route(L, thr).num_slots + 4096
+    rws = torch.empty(et.route_workspace_bytes(T, E), dtype=torch.uint8, device=dev)
+    fws = torch.empty(et.router_route_workspace_bytes(T, E), dtype=torch.uint8, device=dev)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    t_gemm = timed(lambda: et.router_logits(X, Wr, out=L))
+    t_route = timed(lambda: et.route(L, thr, slot_capacity=cap, workspace=rws))
+    t_fused = timed(lambda: et.router_route(X, Wr, thr, slot_capacity=cap, workspace=fws))
+    t_torch = timed(lambda: torch.nn.functional.linear(X, Wr))
+    nbytes = T * d * 2 + E * d * 2 + T * E * 4
+    gbs = nbytes / (t_gemm * 1e-6) / 1e9
+    return {"kernel": "router_logits_kernel", "T": T, "d": d, "E": E, "us": round(t_gemm, 2),
+            "algorithmic_bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs * 1e9 / HBM_PEAK, 4),
+            "TFLOP/s": round(2.0 * T * d * E / (t_gemm * 1e-6) / 1e12, 1),
+            "fused_route_us": round(t_fused, 2), "logits_then_route_us": round(t_gemm + t_route, 2),
+            "torch_linear_bf16_us": round(t_torch, 2)}
 
 
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
@@ -288,6 +333,13 @@ def main() -> int:
               f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
               f"{dyn['mean_k_last_step']}", file=sys.stderr)
 
+    rp = None
+    if act == torch.bfloat16 and E <= 256:
+        rp = router_producer(et, dev, stream, X, E)
+        print(f"  router producer: logits {rp['us']:.1f} us ({rp['GB/s']:.0f} GB/s, {100 * rp['frac']:.1f}% of "
+              f"peak; torch bf16 linear {rp['torch_linear_bf16_us']:.1f} us), fused route {rp['fused_route_us']:.1f}"
+              f" us vs logits + route {rp['logits_then_route_us']:.1f} us", file=sys.stderr)
+
     cpu = None
     if args.cpu_tokens > 0:
         cpu = cpu_baseline(args.workload, args.seed, min(args.cpu_tokens, T))
@@ -315,6 +367,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "copy_ceiling": copy_ref,
         "threshold_dynamics": dyn,
+        "router_producer": rp,
         "kernels": kernels,
     }
     for name in STAGES:
