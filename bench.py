@@ -7,8 +7,10 @@ resident in HBM before timing starts:
     combine_fwd      Y  = sum_s gate[s] * Yp[s]
     combine_bwd      dYp = gate * dY[token], dgate = <dY, Yp>, dlogits (router grad)
     dispatch_bwd     dX = sum_s dXp[s]
-The router producer (router logits GEMM, fused producer + routing) is
-measured separately after the timed steps and reported in "router_producer".
+The router producer (router logits GEMM, fused producer + routing) and its
+backward (dispatch backward with the router input gradient, router weight
+gradient) are measured separately after the timed steps and reported in
+"router_producer" and "router_backward".
 Yp and dXp are separate resident buffers standing in for the expert FFN's
 output and input-gradient (the FFN itself is not part of the path).
 
@@ -171,6 +173,50 @@ def router_producer(et, dev, stream, X, E: int, reps: int = 10) -> dict:
             "TFLOP/s": round(2.0 * T * d * E / (t_gemm * 1e-6) / 1e12, 1),
             "fused_route_us": round(t_fused, 2), "logits_then_route_us": round(t_gemm + t_route, 2),
             "torch_linear_bf16_us": round(t_torch, 2)}
+
+
+def router_backward(et, dev, stream, plan, X, DXP, DGATE, DL, reps: int = 10) -> dict:
+    """The router producer's backward on the workload's step buffers: the
+    dispatch backward with the router's input gradient fused in (against the
+    plain dispatch backward), and the router weight gradient dW = dlogits^T X
+    (against torch's float32 matmul).  Measured after the timed step."""
+    import torch
+    T, d = X.shape
+    E = plan.num_experts
+    g = torch.Generator(device=dev)
+    g.manual_seed(4243)
+    Wr = (torch.randn(E, d, device=dev, generator=g) * d ** -0.5).to(X.dtype)
+    dx = torch.empty(T, d, dtype=X.dtype, device=dev)
+    ws = torch.empty(max(1, int(et.lib().et_dispatch_bwd_router_workspace_bytes(plan.rows))), dtype=torch.uint8,
+                     device=dev)
+    dw = torch.empty(E, d, dtype=torch.float32, device=dev)
+    wws = torch.empty(max(16, int(et.lib().et_router_wgrad_workspace_bytes(T, d, E))), dtype=torch.uint8,
+                      device=dev)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    t_plain = timed(lambda: et.dispatch_backward(DXP, plan, out=dx))
+    t_fused = timed(lambda: et.dispatch_backward(DXP, plan, out=dx, router_weight=Wr, dgate=DGATE, workspace=ws))
+    out = {"dispatch_bwd_us": round(t_plain, 2), "dispatch_bwd_router_us": round(t_fused, 2)}
+    if X.dtype == torch.bfloat16 and E <= 256:
+        t_wg = timed(lambda: et.router_weight_grad(DL, X, out=dw, workspace=wws))
+        t_torch = timed(lambda: torch.mm(DL.t(), X.float()))
+        nbytes = T * d * 2 + T * E * 4 + E * d * 4
+        gbs = nbytes / (t_wg * 1e-6) / 1e9
+        out.update({"router_wgrad_us": round(t_wg, 2), "router_wgrad_GB/s": round(gbs, 1),
+                    "router_wgrad_frac": round(gbs * 1e9 / HBM_PEAK, 4),
+                    "torch_mm_f32_wgrad_us": round(t_torch, 2)})
+    return out
 
 
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
@@ -340,6 +386,13 @@ def main() -> int:
               f"peak; torch bf16 linear {rp['torch_linear_bf16_us']:.1f} us), fused route {rp['fused_route_us']:.1f}"
               f" us vs logits + route {rp['logits_then_route_us']:.1f} us", file=sys.stderr)
 
+    plan_obj = et.RoutingPlan(counts, eoff, toff, st, sg, ts, T, E, S, S)
+    rb = router_backward(et, dev, stream, plan_obj, X, DXP, DGATE, DL)
+    print(f"  router backward: dispatch_bwd {rb['dispatch_bwd_us']:.1f} us -> with the router input gradient "
+          f"{rb['dispatch_bwd_router_us']:.1f} us" + (f"; dW {rb['router_wgrad_us']:.1f} us "
+          f"({100 * rb['router_wgrad_frac']:.1f}% of peak; torch f32 mm {rb['torch_mm_f32_wgrad_us']:.1f} us)"
+          if "router_wgrad_us" in rb else ""), file=sys.stderr)
+
     cpu = None
     if args.cpu_tokens > 0:
         cpu = cpu_baseline(args.workload, args.seed, min(args.cpu_tokens, T))
@@ -368,6 +421,7 @@ def main() -> int:
         "copy_ceiling": copy_ref,
         "threshold_dynamics": dyn,
         "router_producer": rp,
+        "router_backward": rb,
         "kernels": kernels,
     }
     for name in STAGES:

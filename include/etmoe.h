@@ -145,6 +145,26 @@ int et_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const int32_t
                     int64_t num_tokens, int64_t d, int dtype, int64_t slot_capacity,
                     void* dx, void* stream);
 
+/* Bytes of device workspace et_dispatch_bwd_router needs (8 per slot of capacity). */
+size_t et_dispatch_bwd_router_workspace_bytes(int64_t slot_capacity);
+
+/*
+ * Dispatch backward plus the router's input gradient, one pass:
+ *   dX[t, c] = cast(acc), acc = 0; for t's slots s in ascending expert order, e = e(s):
+ *       acc = acc + dXp[s, c];   acc = fma(dl(s), W[e, c], acc)          (binary32)
+ *   dl(s) = dgate[s] * (g * (1 - g)), g = slot_gate[s]  -- the dlogits[t, e]
+ *   entry of et_combine_bwd, so dX = dispatch backward + dlogits . W.
+ *   w_router [E, d] is the router weight, in the dtype of dxp/dx.  dgate is
+ *   et_combine_bwd's output.  expert_offsets gives each slot's expert.
+ * Implements the dispatch backward fused with the router producer's input
+ * gradient (no reference counterpart).
+ */
+int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
+                           int64_t num_tokens, int64_t d, int dtype, int64_t slot_capacity,
+                           const float* slot_gate, const float* dgate, const int32_t* expert_offsets,
+                           int64_t num_experts, const void* w_router, void* dx, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* Bytes of device workspace et_threshold_update needs for T tokens and E experts
  * (it holds the T*E score keys and the radix-select histograms). */
 size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
@@ -178,6 +198,23 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
  */
 int et_router_logits(const void* x, const void* w, int64_t num_tokens, int64_t d, int64_t num_experts,
                      float* logits, void* stream);
+
+/* Bytes of device workspace et_router_wgrad needs (per-split partial dW tiles;
+ * 0 for invalid sizes). */
+size_t et_router_wgrad_workspace_bytes(int64_t num_tokens, int64_t d, int64_t num_experts);
+
+/*
+ * Router weight gradient:  dw[e, c] = sum_t dlogits[t, e] * x[t, c]  (f32 [E, d])
+ *   dlogits f32 [T, E] (et_combine_bwd's output), x bf16 [T, d] (16-byte
+ *   aligned, d a multiple of 8 below 2^22, T*d below 2^30, T*E below 2^29).
+ * On the matrix cores with dl split into two bf16 terms (hi + lo, ~16 bits
+ * more than bf16), binary32 accumulation; the token sum is split over blocks
+ * and the partials are added in a fixed order, so repeated calls give
+ * identical bits.  Exact for integer-valued inputs whose sums stay below 2^24.
+ * Implements the router producer's weight gradient (no reference counterpart).
+ */
+int et_router_wgrad(const float* dlogits, const void* x, int64_t num_tokens, int64_t d, int64_t num_experts,
+                    float* dw, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace et_router_route needs for T tokens and E experts
  * (0 if E is outside [1, ET_MAX_ROUTER_EXPERTS]). */

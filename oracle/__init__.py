@@ -65,6 +65,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_combine_fwd.argtypes = [_p, _p, _p, _p, _i64, _i64, ctypes.c_int, _p]
         L.oracle_dispatch_bwd.restype = None
         L.oracle_dispatch_bwd.argtypes = [_p, _p, _p, _i64, _i64, ctypes.c_int, _p]
+        L.oracle_dispatch_bwd_router.restype = None
+        L.oracle_dispatch_bwd_router.argtypes = [_p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i64, ctypes.c_int, _p]
         L.oracle_combine_bwd.restype = None
         L.oracle_combine_bwd.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64,
                                          ctypes.c_int, _p, _p, _p]
@@ -205,6 +207,23 @@ def dispatch_bwd(dxp: np.ndarray, r: Routing, T: int) -> np.ndarray:
     d = dxp.shape[1]
     dx = np.zeros((T, d), dxp.dtype)
     lib().oracle_dispatch_bwd(_ptr(dxp), _ptr(r.token_offsets), _ptr(r.token_slot), T, d, dt, _ptr(dx))
+    return dx
+
+
+def dispatch_bwd_router(dxp: np.ndarray, r: Routing, T: int, dgate: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """dX = dispatch backward + dlogits . W through the routed pairs, with the
+    per-slot dl = dgate * (g * (1 - g)) (see oracle_dispatch_bwd_router)."""
+    dt = _act_dt(dxp)
+    assert _act_dt(w) == dt
+    dxp = np.ascontiguousarray(dxp)
+    w = np.ascontiguousarray(w)
+    dgate = np.ascontiguousarray(dgate, np.float32)
+    d = dxp.shape[1]
+    E = w.shape[0]
+    dx = np.zeros((T, d), dxp.dtype)
+    lib().oracle_dispatch_bwd_router(_ptr(dxp), _ptr(r.token_offsets), _ptr(r.token_slot),
+                                     _ptr(r.expert_offsets), E, _ptr(r.slot_gate), _ptr(dgate), _ptr(w),
+                                     T, d, dt, _ptr(dx))
     return dx
 
 

@@ -251,6 +251,36 @@ void oracle_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const in
     oracle_combine_fwd(dxp, NULL, token_offsets, token_slot, T, d, dt, dx);
 }
 
+/* Dispatch backward plus the router's input gradient through the routed
+ * logits.  dX[t,c] = cast(acc), acc = 0; for each slot s of t in ascending
+ * expert order, with e = the expert of s (expert_offsets[e] <= s <
+ * expert_offsets[e+1]), g = gate[s] and dl = dgate[s] * (g * (1 - g)) in
+ * binary32 (the dlogits[t,e] value of combine backward for this dgate):
+ *     acc = acc + dXp[s,c];   acc = fmaf(dl, W[e,c], acc)
+ * W is the router weight [E, d] in the activation dtype. */
+void oracle_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
+                                const int32_t* expert_offsets, int64_t E, const float* gate,
+                                const float* dgate, const void* w, int64_t T, int64_t d, int dt, void* dx)
+{
+    float* acc = (float*)malloc((size_t)(d ? d : 1) * sizeof(float));
+    for (int64_t t = 0; t < T; ++t) {
+        for (int64_t c = 0; c < d; ++c) acc[c] = 0.0f;
+        for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j) {
+            int64_t s = token_slot[j];
+            int64_t e = 0;
+            while (e + 1 < E && expert_offsets[e + 1] <= s) ++e;
+            float g = gate[s];
+            float dl = dgate[s] * (g * (1.0f - g));
+            for (int64_t c = 0; c < d; ++c) {
+                acc[c] = acc[c] + load_elem(dxp, s * d + c, dt);
+                acc[c] = fmaf(dl, load_elem(w, e * d + c, dt), acc[c]);
+            }
+        }
+        for (int64_t c = 0; c < d; ++c) store_elem(dx, t * d + c, acc[c], dt);
+    }
+    free(acc);
+}
+
 /* Backward of combine for slot s (token t = sorted_token[s], expert e):
  *   dYp[s,c]   = cast(gate[s] * dY[t,c])       one binary32 multiply, then cast
  *   dgate[s]   = sum_c dY[t,c] * Yp[s,c]        (accumulated here in double; the

@@ -20,6 +20,7 @@ from .expert_threshold import (  # noqa: F401
     router_logits,
     router_route,
     router_route_workspace_bytes,
+    router_weight_grad,
     threshold_update_,
     threshold_workspace_bytes,
 )

@@ -207,11 +207,16 @@ __global__ __launch_bounds__(kRowThreads) void dispatch_fwd_elem(
 
 constexpr int kGatherWaves = 2;
 
-template <int DT, bool GATE>
+// ROUTER (dispatch backward only): every slot also adds dl * W[e] with the
+// slot's router-logit gradient dl and expert e, read per token-list entry
+// from rl_dl / rl_e, and the router weight rows W (same dtype and row length
+// as yp; L2-resident).
+template <int DT, bool GATE, bool ROUTER = false>
 __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
     const char* __restrict__ yp, const float* __restrict__ gate, int t_base, int t_end, int64_t nch,
     uint32_t npieces, const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot,
-    int64_t cap, char* __restrict__ y)
+    int64_t cap, char* __restrict__ y, const int32_t* __restrict__ rl_e = nullptr,
+    const float* __restrict__ rl_dl = nullptr, const char* __restrict__ wr = nullptr)
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
@@ -226,20 +231,31 @@ __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
         const int my = load_slot_block(tok_slot, jb, sp.j1);
         const int n = min(kWave, sp.j1 - jb);
+        int mye = 0;
+        float myd = 0.0f;
+        if constexpr (ROUTER) {
+            const int j = jb + lane_id();
+            mye = j < sp.j1 ? rl_e[j] : 0;
+            myd = j < sp.j1 ? rl_dl[j] : 0.0f;
+        }
         // Walk the valid slots; the load of the next slot's chunk is issued
         // at the end of the current slot's iteration.  (Issuing it before the
         // current slot's arithmetic, a two-deep pipeline, measured slower.)
         int u = 0;
         int s = -1;
-        v4u w = {0u, 0u, 0u, 0u};
+        v4u w = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
         for (; u < n; ++u) {
             s = __builtin_amdgcn_readlane(my, u);
             if (s >= 0 && (int64_t)s < cap) break;
         }
-        if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+        if (u < n && on) {
+            w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+            if constexpr (ROUTER) wv = ld16(wr + (int64_t)__builtin_amdgcn_readlane(mye, u) * rb + idx * 16);
+        }
         while (u < n) {
             const int cur = s;
-            const v4u wc = w;
+            const int ucur = u;
+            const v4u wc = w, wvc = wv;
             for (++u; u < n; ++u) {
                 s = __builtin_amdgcn_readlane(my, u);
                 if (s >= 0 && (int64_t)s < cap) break;
@@ -250,8 +266,18 @@ __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
                 P::unpack(wc, f);
 #pragma unroll
                 for (int i = 0; i < N; ++i) acc[i] = __builtin_fmaf(g, f[i], acc[i]);
+                if constexpr (ROUTER) {
+                    const float dl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myd), ucur));
+                    P::unpack(wvc, f);
+#pragma unroll
+                    for (int i = 0; i < N; ++i) acc[i] = __builtin_fmaf(dl, f[i], acc[i]);
+                }
             }
-            if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+            if (u < n && on) {
+                w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+                if constexpr (ROUTER)
+                    wv = ld16(wr + (int64_t)__builtin_amdgcn_readlane(mye, u) * rb + idx * 16);
+            }
         }
     }
     if (on) st16_nt(y + (int64_t)sp.t * rb + idx * 16, P::pack(acc));
@@ -261,7 +287,8 @@ template <int DT>
 __global__ __launch_bounds__(kRowThreads) void combine_fwd_elem(
     const char* __restrict__ yp, const float* __restrict__ gate, int T, int64_t d,
     const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, int64_t cap,
-    char* __restrict__ y)
+    char* __restrict__ y, const int32_t* __restrict__ rl_e = nullptr, const float* __restrict__ rl_dl = nullptr,
+    const char* __restrict__ wr = nullptr)
 {
     TokenSpan sp;
     if (!token_span(T, tok_off, cap, sp)) return;
@@ -273,6 +300,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_fwd_elem(
             if (s < 0 || (int64_t)s >= cap) continue;
             const float g = gate ? gate[s] : 1.0f;
             acc = __builtin_fmaf(g, load_elem<DT>(yp, (int64_t)s * d + c), acc);
+            if (wr) acc = __builtin_fmaf(rl_dl[j], load_elem<DT>(wr, (int64_t)rl_e[j] * d + c), acc);
         }
         store_elem<DT>(y, (int64_t)sp.t * d + c, acc);
     }
@@ -487,6 +515,35 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_elem(
 // host side
 // ---------------------------------------------------------------------------
 
+// Router-gradient terms of dispatch backward, per token-list entry j (token
+// order): the slot s = tok_slot[j], its expert e(s), and dl = dgate[s] *
+// (g * (1 - g)) with g = gate[s] -- the same binary32 expression as the
+// dlogits entry of combine backward.  Entries past min(S, cap), or whose slot
+// is dropped by an undersized capacity, get e = 0 and dl = 0.
+__global__ __launch_bounds__(kFinishThreads) void router_terms_kernel(
+    const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff, int E, const float* __restrict__ gate,
+    const float* __restrict__ dgate, int64_t cap, int32_t* __restrict__ rl_e, float* __restrict__ rl_dl)
+{
+    extern __shared__ int32_t eo[];                                     // [E + 1]
+    for (int e = threadIdx.x; e <= E; e += kFinishThreads) eo[e] = eoff[e];
+    __syncthreads();
+    const int64_t j = (int64_t)blockIdx.x * kFinishThreads + threadIdx.x;
+    const int64_t S = min((int64_t)eo[E], cap);
+    if (j >= cap) return;
+    int e = 0;
+    float dl = 0.0f;
+    if (j < S) {
+        const int s = tok_slot[j];
+        if (s >= 0 && (int64_t)s < cap) {
+            e = expert_of_slot(eo, E, s);
+            const float g = gate[s];
+            dl = dgate[s] * (g * (1.0f - g));
+        }
+    }
+    rl_e[j] = e;
+    rl_dl[j] = dl;
+}
+
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 static int elem_bytes(int dtype) { return dtype == ET_DTYPE_BF16 ? 2 : 4; }
@@ -593,6 +650,60 @@ extern "C" int et_dispatch_bwd(const void* dxp, const int32_t* token_offsets, co
                                int64_t T, int64_t d, int dtype, int64_t cap, void* dx, void* stream)
 {
     return combine_like("et_dispatch_bwd", dxp, nullptr, token_offsets, token_slot, T, d, dtype, cap, dx, stream);
+}
+
+static size_t router_terms_bytes(int64_t cap) { return cap > 0 ? 2 * ((size_t(cap) * 4 + 255) & ~size_t(255)) : 0; }
+
+extern "C" size_t et_dispatch_bwd_router_workspace_bytes(int64_t slot_capacity)
+{
+    return slot_capacity < 0 ? 0 : router_terms_bytes(slot_capacity);
+}
+
+extern "C" int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
+                                      int64_t T, int64_t d, int dtype, int64_t cap, const float* slot_gate,
+                                      const float* dgate, const int32_t* expert_offsets, int64_t E,
+                                      const void* w_router, void* dx, void* workspace, size_t workspace_bytes,
+                                      void* stream)
+{
+    const char* fn = "et_dispatch_bwd_router";
+    if (int rc = check_common(fn, T, d, dtype, cap, token_offsets, token_slot)) return rc;
+    if (E < 1 || E > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_EXPERTS) + "]");
+    if (!expert_offsets) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null expert_offsets");
+    if (T == 0 || d == 0) return ET_OK;
+    if (!dx || (cap > 0 && (!dxp || !slot_gate || !dgate || !w_router || !workspace)))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null input/output/workspace");
+    const size_t need = router_terms_bytes(cap);
+    if (workspace_bytes < need)
+        return fail(ET_ERR_WORKSPACE_TOO_SMALL, std::string(fn) + ": workspace needs " + std::to_string(need) +
+                                                    " bytes, got " + std::to_string(workspace_bytes));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t* rl_e = static_cast<int32_t*>(workspace);
+    float* rl_dl = reinterpret_cast<float*>(static_cast<char*>(workspace) + need / 2);
+    if (cap > 0) {
+        const unsigned nb = (unsigned)((cap + kFinishThreads - 1) / kFinishThreads);
+        router_terms_kernel<<<dim3(nb), dim3(kFinishThreads), size_t(E + 1) * 4, s>>>(
+            token_slot, expert_offsets, (int)E, slot_gate, dgate, cap, rl_e, rl_dl);
+        if (int rc = check_launch("router_terms_kernel")) return rc;
+    }
+    const int64_t rb = d * elem_bytes(dtype);
+    const char* dxpc = static_cast<const char*>(dxp);
+    const char* wrc = static_cast<const char*>(w_router);
+    char* dxc = static_cast<char*>(dx);
+    if (rb % 16 == 0 && aligned16(dxp) && aligned16(dx) && aligned16(w_router)) {
+        const int64_t nch = rb / 16;
+        const int64_t np = (nch + kWave - 1) / kWave;
+        for_each_piece_launch(T, np, kGatherWaves, [&](dim3 grid, int t0, int t1) {
+            ET_SWITCH_DT(dtype, combine_fwd_vec<DT, false, true><<<grid, dim3(kGatherWaves * kWave), 0, s>>>(
+                                    dxpc, nullptr, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap, dxc,
+                                    rl_e, rl_dl, wrc));
+        });
+    } else {
+        ET_SWITCH_DT(dtype, combine_fwd_elem<DT><<<row_grid(T), dim3(kRowThreads), 0, s>>>(
+                                dxpc, nullptr, (int)T, d, token_offsets, token_slot, cap, dxc, rl_e, rl_dl, wrc));
+    }
+    return check_launch(fn);
 }
 
 static bool bwd_vector_path(int64_t d, int dtype) { return d > 0 && (d * elem_bytes(dtype)) % 16 == 0; }

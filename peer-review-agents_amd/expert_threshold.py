@@ -270,9 +270,17 @@ def combine_backward(dy: torch.Tensor, yp: torch.Tensor, plan: RoutingPlan, *,
     return dyp, dgate, dl
 
 
-def dispatch_backward(dxp: torch.Tensor, plan: RoutingPlan,
-                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Backward of dispatch: dX[t] = sum of dXp over t's slots (ascending expert)."""
+def dispatch_backward(dxp: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = None, *,
+                      router_weight: Optional[torch.Tensor] = None, dgate: Optional[torch.Tensor] = None,
+                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Backward of dispatch: dX[t] = sum of dXp over t's slots (ascending expert).
+
+    With ``router_weight`` (W [E, d], the dtype of dxp) and ``dgate`` (from
+    :func:`combine_backward`), the router's input gradient through the routed
+    logits is added in the same pass: per slot s of expert e,
+    dX[t] += dl(s) * W[e] with dl(s) = dgate[s] * g * (1 - g), the dlogits
+    entry of combine_backward -- i.e. dX + dlogits @ W.
+    """
     dt = _require_act(dxp, "dxp")
     dev = dxp.device
     _check_plan(plan, dev)
@@ -280,11 +288,63 @@ def dispatch_backward(dxp: torch.Tensor, plan: RoutingPlan,
         raise ValueError(f"dxp has {dxp.shape[0]} rows, plan has {plan.rows} slots")
     T, d = plan.num_tokens, dxp.shape[1]
     dx = _out_or_new(out, (T, d), dxp.dtype, dev, "out")
+    if (router_weight is None) != (dgate is None):
+        raise ValueError("router_weight and dgate go together")
+    if router_weight is None:
+        with torch.cuda.device(dev):
+            rc = lib().et_dispatch_bwd(_vp(dxp), _vp(plan.token_offsets), _vp(plan.token_slot), T, d, dt,
+                                       plan.rows, _vp(dx), _stream(dev))
+        check("et_dispatch_bwd", rc)
+        return dx
+    E = plan.num_experts
+    _require(router_weight, "router_weight", dxp.dtype, 2, dev)
+    if tuple(router_weight.shape) != (E, d):
+        raise ValueError(f"router_weight must have shape {(E, d)}, got {tuple(router_weight.shape)}")
+    _require(dgate, "dgate", torch.float32, 1, dev)
+    if dgate.shape[0] != plan.rows:
+        raise ValueError(f"dgate has {dgate.shape[0]} entries, plan has {plan.rows} slots")
+    wsb = int(lib().et_dispatch_bwd_router_workspace_bytes(plan.rows))
+    if workspace is None:
+        workspace = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace must hold {wsb} bytes on {dev}")
     with torch.cuda.device(dev):
-        rc = lib().et_dispatch_bwd(_vp(dxp), _vp(plan.token_offsets), _vp(plan.token_slot), T, d, dt,
-                                   plan.rows, _vp(dx), _stream(dev))
-    check("et_dispatch_bwd", rc)
+        rc = lib().et_dispatch_bwd_router(_vp(dxp), _vp(plan.token_offsets), _vp(plan.token_slot), T, d, dt,
+                                          plan.rows, _vp(plan.slot_gate), _vp(dgate), _vp(plan.expert_offsets), E,
+                                          _vp(router_weight), _vp(dx), _vp(workspace), wsb, _stream(dev))
+    check("et_dispatch_bwd_router", rc)
     return dx
+
+
+def router_weight_grad(dlogits: torch.Tensor, x: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                       workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Router weight gradient dW = dlogits^T X (float32 [E, d]) from the f32
+    router-logit gradient [T, E] and the bf16 router input [T, d]."""
+    _require(dlogits, "dlogits", torch.float32, 2)
+    dev = dlogits.device
+    _require(x, "x", torch.bfloat16, 2, dev)
+    T, E = dlogits.shape
+    if x.shape[0] != T:
+        raise ValueError(f"x has {x.shape[0]} tokens, dlogits has {T}")
+    d = x.shape[1]
+    if not 1 <= E <= ET_MAX_ROUTER_EXPERTS:
+        raise ValueError(f"num_experts must be in [1, {ET_MAX_ROUTER_EXPERTS}], got {E}")
+    if d < 8 or d % 8 or d >= 1 << 22:
+        raise ValueError(f"d must be a positive multiple of 8 below 2^22, got {d}")
+    if T * d >= 1 << 30 or T * E >= 1 << 29:
+        raise ValueError("x must be below 2^30 elements and dlogits below 2^29")
+    dw = _out_or_new(out, (E, d), torch.float32, dev, "out")
+    if x.data_ptr() % 16 or dw.data_ptr() % 16:
+        raise ValueError("x and out must be 16-byte aligned")
+    wsb = int(lib().et_router_wgrad_workspace_bytes(T, d, E))
+    if workspace is None:
+        workspace = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace must hold {wsb} bytes on {dev}")
+    with torch.cuda.device(dev):
+        rc = lib().et_router_wgrad(_vp(dlogits), _vp(x), T, d, E, _vp(dw), _vp(workspace), wsb, _stream(dev))
+    check("et_router_wgrad", rc)
+    return dw
 
 
 # --------------------------------------------------------------------------- #

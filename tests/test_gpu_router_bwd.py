@@ -1,0 +1,201 @@
+"""Backward of the router producer on the GPU.
+
+dispatch_backward(..., router_weight=W, dgate=dgate) adds the router's input
+gradient dlogits . W through the routed pairs in the same pass as the dispatch
+backward; it is held bit-exact to the CPU oracle (oracle_dispatch_bwd_router,
+pinned in test_oracle.py) and checked against the composition with
+combine_backward's dlogits.
+
+router_weight_grad(dlogits, X) = dlogits^T X is pinned by what the arithmetic
+fixes: exact on integer-valued inputs whose sums stay below 2^24 (the hi/lo
+split of dl is exact for bf16-representable dl), within the rigorous binary32
+bound of the float64 product on random inputs, and bit-identical across calls.
+torch supplies the float64 products as the checker.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import dev_f32, host
+
+W = importlib.import_module("peer-review-agents_amd.workloads")
+
+pytestmark = pytest.mark.gpu
+
+
+def _route(et, orc, dev, T, E, seed, q=0.8):
+    rng = np.random.default_rng(seed)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    thr = np.quantile(1.0 / (1.0 + np.exp(-lg.astype(np.float64))), q, axis=0).astype(np.float32)
+    return et.route(dev_f32(lg, dev), dev_f32(thr, dev)), orc.route(lg, thr)
+
+
+def _act(rng, shape, dt, dev, orc):
+    a = rng.standard_normal(shape).astype(np.float32)
+    if dt == "bf16":
+        bits = orc.f32_to_bf16(a)
+        return torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16), bits
+    return torch.from_numpy(a).to(dev), a
+
+
+def _bits(a):
+    a = host(a) if isinstance(a, torch.Tensor) else np.ascontiguousarray(a)
+    return a.view(np.uint16) if a.dtype == np.uint16 else a.view(np.uint32)
+
+
+@pytest.mark.parametrize("T,d,E,dt", [
+    (300, 64, 8, "f32"), (513, 520, 40, "bf16"), (1000, 1024, 128, "bf16"), (200, 4096, 16, "bf16"),
+    (257, 12, 5, "bf16"), (150, 7, 4, "f32"), (700, 96, 64, "f32"),
+])
+def test_dispatch_bwd_router_matches_oracle(et, orc, dev, T, d, E, dt):
+    print(f"dispatch_bwd_router T={T} d={d} E={E} {dt}", flush=True)
+    plan, r = _route(et, orc, dev, T, E, T + d + E)
+    rng = np.random.default_rng(7 + d)
+    dxp, dxp_h = _act(rng, (plan.num_slots, d), dt, dev, orc)
+    w, w_h = _act(rng, (E, d), dt, dev, orc)
+    dgate_h = rng.standard_normal(plan.num_slots).astype(np.float32)
+    dx = et.dispatch_backward(dxp, plan, router_weight=w, dgate=dev_f32(dgate_h, dev))
+    want = orc.dispatch_bwd_router(dxp_h, r, T, dgate_h, w_h)
+    np.testing.assert_array_equal(_bits(dx), _bits(want))
+    # without the router term it is the plain dispatch backward
+    plain = et.dispatch_backward(dxp, plan)
+    np.testing.assert_array_equal(_bits(plain), _bits(orc.dispatch_bwd(dxp_h, r, T)))
+
+
+def test_dispatch_bwd_router_undersized_capacity(et, orc, dev):
+    T, d, E = 400, 64, 16
+    rng = np.random.default_rng(3)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    thr = np.full(E, 0.6, np.float32)
+    S = orc.route(lg, thr).num_slots
+    cap = S // 2
+    plan = et.route(dev_f32(lg, dev), dev_f32(thr, dev), slot_capacity=cap)
+    full = et.route(dev_f32(lg, dev), dev_f32(thr, dev))
+    dxp = torch.randn(cap, d, device=dev)
+    w = torch.randn(E, d, device=dev)
+    dgate = torch.randn(cap, device=dev)
+    got = et.dispatch_backward(dxp, plan, router_weight=w, dgate=dgate)
+    # reference: the kept pairs only -- slot s < cap whose token-list entry j < cap
+    ts = host(full.token_slot)
+    to = host(full.token_offsets)
+    eo = host(full.expert_offsets)
+    gate = host(full.slot_gate).astype(np.float32)
+    dxp_h, w_h, dg_h = host(dxp), host(w), host(dgate)
+    ref = np.zeros((T, d))
+    mass = np.zeros((T, d))
+    kept = 0
+    for t in range(T):
+        for j in range(to[t], to[t + 1]):
+            s = ts[j]
+            if j >= cap or s >= cap:
+                continue
+            kept += 1
+            e = int(np.searchsorted(eo, s, side="right") - 1)
+            dl = np.float32(dg_h[s] * np.float32(gate[s] * np.float32(1.0 - gate[s])))
+            ref[t] += dxp_h[s].astype(np.float64) + np.float64(dl) * w_h[e]
+            mass[t] += np.abs(dxp_h[s]) + abs(np.float64(dl)) * np.abs(w_h[e])
+    assert 0 < kept < S
+    k = int(np.diff(to).max())
+    assert np.all(np.abs(host(got) - ref) <= mass * (2 * k + 2) * 2.0 ** -24)
+
+
+def test_dispatch_bwd_router_composes_with_combine_backward(et, dev):
+    """The router term uses exactly combine_backward's dlogits entries:
+    dispatch_backward(router) == dispatch_backward + dlogits @ W (float64 bound)."""
+    T, d, E = 2048, 256, 32
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    L = torch.randn(T, E, device=dev, generator=g)
+    plan = et.route(L, torch.full((E,), 0.7, device=dev))
+    S = plan.num_slots
+    bf = torch.bfloat16
+    yp = torch.randn(S, d, device=dev, generator=g).to(bf)
+    dy = (torch.randn(T, d, device=dev, generator=g) * 0.02).to(bf)
+    dxp = torch.randn(S, d, device=dev, generator=g).to(bf)
+    w = (torch.randn(E, d, device=dev, generator=g) * 0.1).to(bf)
+    _, dgate, dlog = et.combine_backward(dy, yp, plan, need_dlogits=True)
+    got = et.dispatch_backward(dxp, plan, router_weight=w, dgate=dgate).double()
+    base = et.dispatch_backward(dxp, plan).double()
+    ref = torch.zeros(T, d, device=dev, dtype=torch.float64).index_add_(
+        0, plan.sorted_token.long(), dxp.double()) + dlog.double() @ w.double()
+    mass = torch.zeros(T, d, device=dev, dtype=torch.float64).index_add_(
+        0, plan.sorted_token.long(), dxp.double().abs()) + dlog.double().abs() @ w.double().abs()
+    k = int(torch.diff(plan.token_offsets).max())
+    tol = ref.abs() * 2.0 ** -8 + mass * (2 * k + 2) * 2.0 ** -24
+    assert bool(((got - ref).abs() <= tol).all())
+    assert not torch.equal(got, base)
+
+
+# --------------------------------------------------------------------------- #
+# router weight gradient
+# --------------------------------------------------------------------------- #
+
+WGRAD_SHAPES = [  # (T, d, E): ragged token splits, E off the 32-wide tile, d off the 256-column block
+    (1, 8, 1), (100, 264, 40), (4097, 1024, 128), (33001, 136, 100), (7000, 72, 256), (65536, 512, 128),
+    (333, 4096, 8),
+]
+
+
+@pytest.mark.parametrize("T,d,E", WGRAD_SHAPES)
+def test_router_wgrad_exact_on_integer_inputs(et, dev, T, d, E):
+    print(f"router_wgrad integer T={T} d={d} E={E}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(T + d + E)
+    dl = torch.randint(-3, 4, (T, E), generator=g, device=dev).float()
+    dl[torch.rand(T, E, generator=g, device=dev) < 0.8] = 0.0          # sparse, as routed dlogits are
+    x = torch.randint(-4, 5, (T, d), generator=g, device=dev).to(torch.bfloat16)
+    dw = et.router_weight_grad(dl, x)
+    want = dl.double().T @ x.double()
+    assert dw.dtype == torch.float32 and tuple(dw.shape) == (E, d)
+    assert torch.equal(dw.double(), want)
+
+
+def test_router_wgrad_random_within_bound_and_deterministic(et, dev):
+    T, d, E = 16384, 2048, 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    dl = torch.randn(T, E, generator=g, device=dev) * 1e-3
+    x = torch.randn(T, d, generator=g, device=dev).to(torch.bfloat16)
+    dw = et.router_weight_grad(dl, x)
+    dw2 = et.router_weight_grad(dl, x)
+    assert torch.equal(dw.view(torch.int32), dw2.view(torch.int32))
+    ref = dl.double().T @ x.double()
+    mass = dl.double().abs().T @ x.double().abs()
+    err = (dw.double() - ref).abs()
+    # dl = hi + lo + r with |r| <= 2^-17 |dl|; binary32 sums of at most 2 T terms
+    assert bool((err <= (2.0 ** -17 + 2 * T * 2.0 ** -24) * mass).all())
+    assert float((err / mass).mean()) < 2.0 ** -16
+
+
+def test_router_wgrad_full_size_c3(et, dev):
+    cfg = W.CONFIGS["C3"]
+    T, d, E = cfg["T"], cfg["d"], cfg["E"]
+    print(f"router_wgrad C3 T={T} d={d} E={E}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    dl = torch.randn(T, E, generator=g, device=dev) * 1e-3
+    dl[torch.rand(T, E, generator=g, device=dev) < 0.9] = 0.0
+    x = torch.randn(T, d, generator=g, device=dev).to(torch.bfloat16)
+    dw = et.router_weight_grad(dl, x)
+    ref = torch.zeros(E, d, device=dev, dtype=torch.float64)
+    mass = torch.zeros(E, d, device=dev, dtype=torch.float64)
+    for i in range(0, T, 8192):
+        ref += dl[i:i + 8192].double().T @ x[i:i + 8192].double()
+        mass += dl[i:i + 8192].double().abs().T @ x[i:i + 8192].double().abs()
+    err = (dw.double() - ref).abs()
+    assert bool((err <= (2.0 ** -17 + 2 * T * 2.0 ** -24) * mass).all())
+    assert float((err / mass).mean()) < 2.0 ** -16
+
+
+def test_router_wgrad_empty_and_validation(et, dev):
+    x = torch.zeros(0, 64, device=dev, dtype=torch.bfloat16)
+    dw = et.router_weight_grad(torch.zeros(0, 8, device=dev), x, out=torch.full((8, 64), 7.0, device=dev))
+    assert bool((dw == 0).all())
+    with pytest.raises(ValueError):
+        et.router_weight_grad(torch.zeros(4, 8, device=dev), torch.zeros(5, 64, device=dev, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        et.router_weight_grad(torch.zeros(4, 8, device=dev), torch.zeros(4, 64, device=dev))
+    with pytest.raises(ValueError):
+        et.router_weight_grad(torch.zeros(4, 300, device=dev), torch.zeros(4, 64, device=dev, dtype=torch.bfloat16))

@@ -302,6 +302,57 @@ def test_backward_against_float64_autograd(orc, dt):
     assert np.all(dl[unrouted] == 0)
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_dispatch_bwd_router_reduces_and_is_exact_on_integers(orc, dt):
+    """dX = dispatch backward + dlogits . W: with W = 0 or dgate = 0 it is the
+    dispatch backward bit for bit; with all logits 0 every gate is 0.5, so
+    dl = dgate / 4 and integer-valued inputs give the exact integer sum
+    sum_s dXp[s] + dl(s) W[e(s)], which pins the expert row each slot adds."""
+    cvt = orc.bf16_to_f32 if dt == "bf16" else (lambda a: a)
+    enc = orc.f32_to_bf16 if dt == "bf16" else (lambda a: a)
+    T, E, d = 90, 7, 20
+    r, _ = _plan(orc, T, E, 30, q=0.6)
+    rng = np.random.default_rng(31)
+    dxp = enc(rng.standard_normal((r.num_slots, d)).astype(np.float32))
+    w = enc(rng.standard_normal((E, d)).astype(np.float32))
+    dgate = rng.standard_normal(r.num_slots).astype(np.float32)
+    base = orc.dispatch_bwd(dxp, r, T)
+    np.testing.assert_array_equal(orc.dispatch_bwd_router(dxp, r, T, dgate, np.zeros_like(w)), base)
+    np.testing.assert_array_equal(orc.dispatch_bwd_router(dxp, r, T, np.zeros_like(dgate), w), base)
+    # all scores 0.5, thresholds 0.5: every (t, e) routed, gates 0.5
+    T2, E2, d2 = 40, 5, 12
+    r2 = orc.route(np.zeros((T2, E2), np.float32), np.full(E2, 0.5, np.float32))
+    assert r2.num_slots == T2 * E2 and np.all(r2.slot_gate == 0.5)
+    dxp2 = rng.integers(-8, 9, (r2.num_slots, d2)).astype(np.float32)
+    w2 = rng.integers(-8, 9, (E2, d2)).astype(np.float32)
+    m = rng.integers(-6, 7, r2.num_slots)
+    got = cvt(orc.dispatch_bwd_router(enc(dxp2), r2, T2, (4 * m).astype(np.float32), enc(w2)))
+    ee = np.repeat(np.arange(E2), np.diff(r2.expert_offsets))
+    want = np.zeros((T2, d2), np.int64)
+    np.add.at(want, r2.sorted_token, dxp2.astype(np.int64) + m[:, None] * w2[ee].astype(np.int64))
+    np.testing.assert_array_equal(got, want.astype(np.float32))
+
+
+def test_dispatch_bwd_router_against_float64(orc):
+    T, E, d = 110, 9, 28
+    r, _ = _plan(orc, T, E, 40, q=0.6)
+    rng = np.random.default_rng(41)
+    dxp = rng.standard_normal((r.num_slots, d)).astype(np.float32)
+    w = rng.standard_normal((E, d)).astype(np.float32)
+    dgate = rng.standard_normal(r.num_slots).astype(np.float32)
+    got = orc.dispatch_bwd_router(dxp, r, T, dgate, w)
+    g = r.slot_gate
+    dl = (dgate * (g * (np.float32(1) - g))).astype(np.float32)     # the dlogits entries
+    ee = np.repeat(np.arange(E), np.diff(r.expert_offsets))
+    terms = dxp.astype(np.float64) + dl[:, None].astype(np.float64) * w[ee].astype(np.float64)
+    ref = np.zeros((T, d))
+    mass = np.zeros((T, d))
+    np.add.at(ref, r.sorted_token, terms)
+    np.add.at(mass, r.sorted_token, np.abs(dxp) + np.abs(dl[:, None] * w[ee]))
+    k = np.diff(r.token_offsets).max()
+    assert np.all(np.abs(got - ref) <= mass * (2 * k + 1) * 2.0 ** -24)
+
+
 # --------------------------------------------------------------------------- #
 # EMA threshold update
 # --------------------------------------------------------------------------- #
