@@ -36,6 +36,7 @@ constexpr uint32_t kOutOfRange = 0x80000000u;    // offset past every num_record
 constexpr int kColsPerBlock = 256;               // 32 lanes x 8 consecutive columns
 constexpr int kTilesPerBlock = 4;                // expert tiles (waves) per block; grid z covers the rest
 constexpr int kMaxSplit = 64;
+constexpr int kRing = 2;                         // k-steps of 16 tokens in the load ring
 
 // The 8 x 8 transpose: xr[i] holds token i's columns 0..7 (2 bf16 per dword);
 // bf[j] gets column j's tokens 0..7.
@@ -101,26 +102,33 @@ __global__ __launch_bounds__(kTilesPerBlock * kWave) void router_wgrad_kernel(
             alo[k] = pack_bf16x2(r0, r1);
         }
         const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, ahi), al = __builtin_bit_cast(bf16x8_t, alo);
+        // all hi terms, then all lo terms: the two MFMAs on one accumulator are
+        // 8 apart, so none waits for the previous one's result
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const bf16x8_t b = __builtin_bit_cast(bf16x8_t, bf[j]);
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc[j], 0, 0, 0);
-        }
+        for (int j = 0; j < 8; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, __builtin_bit_cast(bf16x8_t, bf[j]), acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, __builtin_bit_cast(bf16x8_t, bf[j]), acc[j], 0, 0, 0);
     };
 
-    // two k-steps in flight: the loads of step s + 1 are issued before step s
-    // is computed
-    u32x4_t xa[8], xb[8];
-    float da[8], db[8];
-    int t = t_begin;
-    if (t < t_end) load(t, xa, da);
-    for (; t < t_end; t += 32) {
-        load(t + 16, xb, db);
-        compute(xa, da);
-        if (t + 16 >= t_end) break;
-        load(t + 32, xa, da);
-        compute(xb, db);
+    // A ring of kRing k-steps: the loads of step s + kRing - 1 are issued
+    // before step s is computed.  The loop runs whole groups of kRing steps
+    // over the split (its length is a multiple of 16 kRing tokens) with no
+    // exit inside, so the accumulators and the ring keep their registers;
+    // steps past t_end load zeros and add nothing.
+    u32x4_t xr[kRing][8];
+    float dv[kRing][8];
+#pragma unroll
+    for (int p = 0; p < kRing - 1; ++p) load(t_begin + 16 * p, xr[p], dv[p]);
+    for (int t = t_begin; t < t_end; t += 16 * kRing) {
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(t + 16 * (r + kRing - 1), xr[(r + kRing - 1) % kRing], dv[(r + kRing - 1) % kRing]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(xr[r], dv[r]);
+        }
     }
 
     // partial tile: lane (q, h) holds columns c0 .. c0 + 7 (acc[0..7]) of
@@ -176,7 +184,7 @@ WgradPlan wgrad_plan(int64_t T, int64_t d, int64_t E)
     const int64_t max_by_t = std::max<int64_t>(1, (T + 63) / 64);
     p.ks = (int)std::max<int64_t>(1, std::min<int64_t>({want, (int64_t)kMaxSplit, max_by_t}));
     const int64_t per = (T + p.ks - 1) / p.ks;
-    p.tok_per_split = (int)(((per + 31) / 32) * 32);
+    p.tok_per_split = (int)(((per + 16 * kRing - 1) / (16 * kRing)) * (16 * kRing));
     p.ks = (int)std::max<int64_t>(1, (T + p.tok_per_split - 1) / p.tok_per_split);
     return p;
 }
