@@ -106,3 +106,60 @@ def test_moe_layer_trains_with_ema_thresholds(dev):
         assert int(torch.diff(plan.token_offsets).min()) >= 1
     assert not torch.equal(thr0, layer.thr.thr)
     assert bool(((layer.thr.thr > 0) & (layer.thr.thr < 1)).all())
+
+
+def test_manual_bf16_training_step_with_router_kernels(dev):
+    """A bf16 training step with the router on this library's kernels, the way a
+    fused training loop calls them (no autograd through the path):
+      router_logits -> route -> dispatch -> expert FFNs (torch) -> combine;
+      combine_backward -> FFN backward (torch) -> dispatch_backward with the
+      router's input gradient -> router_weight_grad.
+    Output, dX and dW_router against a float64 restatement with the same routed
+    pairs; the bar is the bf16 one (each bf16 rounding on the path is 2^-9)."""
+    et = importlib.import_module("peer-review-agents_amd")
+    T, d, E, h = 512, 128, 16, 64
+    g = torch.Generator().manual_seed(7)
+    bf = torch.bfloat16
+    X = (torch.randn(T, d, generator=g)).to(bf).to(dev)
+    Wr = (torch.randn(E, d, generator=g) * d ** -0.5).to(bf).to(dev)
+    w1 = (torch.randn(E, d, h, generator=g) * d ** -0.5).to(dev)
+    w2 = (torch.randn(E, h, d, generator=g) * h ** -0.5).to(dev)
+    dy = (torch.randn(T, d, generator=g) * 0.1).to(bf).to(dev)
+
+    logits = et.router_logits(X, Wr)
+    thr = torch.quantile(torch.sigmoid(logits.double()), 0.8, dim=0).float().contiguous()
+    plan = et.route(logits, thr)
+    xp = et.dispatch(X, plan)
+    eo = plan.expert_offsets.tolist()
+    xpf = xp.float().requires_grad_(True)
+    yp_parts = [torch.relu(xpf[eo[e]:eo[e + 1]] @ w1[e]) @ w2[e] for e in range(E)]
+    ypf = torch.cat(yp_parts)
+    yp = ypf.detach().to(bf).contiguous()
+    y = et.combine(yp, plan)
+    dyp, dgate, dlogits = et.combine_backward(dy, yp, plan, need_dlogits=True)
+    (dxpf,) = torch.autograd.grad(ypf, xpf, grad_outputs=dyp.float())
+    dx = et.dispatch_backward(dxpf.to(bf).contiguous(), plan, router_weight=Wr, dgate=dgate)
+    dwr = et.router_weight_grad(dlogits, X)
+
+    # float64 restatement on the bf16 inputs, same routed pairs
+    st = plan.sorted_token.long().cpu()
+    ee = torch.repeat_interleave(torch.arange(E), plan.counts.long().cpu())
+    xr = X.cpu().double().requires_grad_(True)
+    wr = Wr.cpu().double().requires_grad_(True)
+    lg = xr @ wr.T
+    gate = torch.sigmoid(lg[st, ee])
+    xs = xr[st]
+    hid = torch.relu(torch.einsum("sd,sdh->sh", xs, w1.cpu().double()[ee]))
+    ys = torch.einsum("sh,shd->sd", hid, w2.cpu().double()[ee])
+    yr = torch.zeros(T, d, dtype=torch.float64).index_add(0, st, gate[:, None] * ys)
+    yr.backward(dy.cpu().double())
+
+    def close(a, b, name, rel):
+        a = a.detach().cpu().double()
+        scale = b.abs().max().item() + 1e-12
+        err = (a - b.detach()).abs().max().item()
+        assert err <= rel * scale, f"{name}: max error {err:.3e} vs scale {scale:.3e}"
+
+    close(y, yr, "y", 2e-2)
+    close(dx, xr.grad, "dX", 3e-2)
+    close(dwr, wr.grad, "dW_router", 3e-2)
