@@ -146,6 +146,26 @@ __device__ __forceinline__ float wave_sum_dpp(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kWave - 1));
 }
 
+// Max over the wave's 64 lanes of an unsigned key, with the DPP moves of
+// wave_sum_dpp (lanes outside a move's source row take 0, the identity of an
+// unsigned max).  Returned wave-uniform.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_mov_u32(uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xf, false);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v)
+{
+    v = max(v, dpp_mov_u32<0xB1>(v));
+    v = max(v, dpp_mov_u32<0x4E>(v));
+    v = max(v, dpp_mov_u32<0x114>(v));
+    v = max(v, dpp_mov_u32<0x118>(v));
+    v = max(v, dpp_mov_u32<0x142, 0xA>(v));
+    v = max(v, dpp_mov_u32<0x143, 0xC>(v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
+}
+
 // Inclusive prefix sum across the wave.
 __device__ __forceinline__ int wave_incl_scan(int v)
 {

@@ -31,7 +31,8 @@ __device__ __forceinline__ void load_thresholds(const float* __restrict__ thr, i
 // Selection of one token: m[g] = ballot(score >= thr) over group g, sc[g] =
 // the lane's score.  A token with no expert gets the argmax expert (NaN lowest,
 // ties to the lowest expert index; lanes past E hold NaN, so an all-NaN token
-// goes to expert 0).  Returns the token's expert count (wave-uniform).
+// goes to expert 0).  Returns the token's expert count (wave-uniform).  Scores
+// are sigmoids, so never negative: their bit patterns order like the values.
 template <int GM>
 __device__ __forceinline__ int select_token(const float (&lg)[GM], const float (&th)[GM], int G,
                                             uint64_t (&m)[GM], float (&sc)[GM])
@@ -45,22 +46,22 @@ __device__ __forceinline__ int select_token(const float (&lg)[GM], const float (
         k += (int)__popcll(m[g]);
     }
     if (k == 0) {
-        float bv = (sc[0] != sc[0]) ? -1.0f : sc[0];
+        // Argmax by two DPP reductions (no LDS round trips).  Keys order the
+        // scores (all >= 0) by their bits, with NaN below every score; each
+        // lane keeps its best group, the lowest on ties.  The wave max of the
+        // keys is the best score; the wave max of ~e over the lanes holding
+        // it is the lowest expert index with that score.
+        uint32_t bk = 0u;
         int be = lane;
 #pragma unroll
-        for (int g = 1; g < GM; ++g) {
+        for (int g = 0; g < GM; ++g) {
             if (g < G) {
-                const float v = (sc[g] != sc[g]) ? -1.0f : sc[g];
-                if (v > bv) { bv = v; be = g * kWave + lane; }
+                const uint32_t key = (sc[g] != sc[g]) ? 0u : f2u(sc[g]) + 1u;
+                if (key > bk) { bk = key; be = g * kWave + lane; }
             }
         }
-#pragma unroll
-        for (int off = kWave / 2; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, kWave);
-            const int oe = __shfl_xor(be, off, kWave);
-            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
-        }
-        be = __builtin_amdgcn_readfirstlane(be);
+        const uint32_t top = wave_max_u32_dpp(bk);
+        be = (int)~wave_max_u32_dpp(bk == top ? ~(uint32_t)be : 0u);
 #pragma unroll
         for (int g = 0; g < GM; ++g) m[g] = (g == (be >> 6)) ? (1ull << (be & (kWave - 1))) : 0ull;
         k = 1;
