@@ -54,14 +54,21 @@ __device__ __forceinline__ void transpose8x8(const u32x4_t (&xr)[8], u32x4_t (&b
 // dW partial of one (column block, token range): wave = expert tile n.
 __global__ __launch_bounds__(kTilesPerBlock * kWave) void router_wgrad_kernel(
     const float* __restrict__ dl, const uint16_t* __restrict__ x, int T, int d, int E, int tok_per_split,
-    float* __restrict__ part)
+    int ncb, int nsplit, float* __restrict__ part)
 {
     const int lane = lane_id();
     const int n = (int)blockIdx.z * kTilesPerBlock + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int q = lane & 31;
     const int h = lane >> 5;
-    const int cb = blockIdx.x;
-    const int ks = blockIdx.y;
+    // XCD-aware block order: consecutive block ids go to the 8 XCDs in turn,
+    // so block id b runs on XCD b % 8.  All column blocks of split ks are put
+    // on XCD ks % 8, and the split's dlogits rows are fetched into one L2
+    // instead of every XCD's.
+    const int b = (int)blockIdx.x;
+    const int xcd = b & 7, slot = b >> 3;
+    const int cb = slot % ncb;
+    const int ks = xcd + 8 * (slot / ncb);
+    if (ks >= nsplit) return;
     const int c0 = cb * kColsPerBlock + 8 * q;      // this lane's 8 columns
     const int e = n * 32 + q;                       // this lane's expert (A rows)
     const int t_begin = ks * tok_per_split;
@@ -232,8 +239,9 @@ extern "C" int et_router_wgrad(const float* dlogits, const void* x, int64_t T, i
                                                     " bytes, got " + std::to_string(workspace_bytes));
     float* part = static_cast<float*>(workspace);
     const int nz = (p.nt + kTilesPerBlock - 1) / kTilesPerBlock;
-    router_wgrad_kernel<<<dim3(p.ncb, p.ks, nz), dim3(std::min(p.nt, kTilesPerBlock) * kWave), 0, s>>>(
-        dlogits, static_cast<const uint16_t*>(x), (int)T, (int)d, (int)E, p.tok_per_split, part);
+    const unsigned nblk = (unsigned)(p.ncb * ((p.ks + 7) / 8) * 8);   // split groups of 8 (one per XCD)
+    router_wgrad_kernel<<<dim3(nblk, 1, nz), dim3(std::min(p.nt, kTilesPerBlock) * kWave), 0, s>>>(
+        dlogits, static_cast<const uint16_t*>(x), (int)T, (int)d, (int)E, p.tok_per_split, p.ncb, p.ks, part);
     if (int rc = check_launch("router_wgrad_kernel")) return rc;
     router_wgrad_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(part, p.ks, n4, dw);
     return check_launch("router_wgrad_reduce_kernel");
