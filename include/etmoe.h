@@ -7,7 +7,10 @@
  * exclusive-scan CSR of expert offsets, a stable permutation of tokens into
  * expert-major slots (ordered by expert, then token id), the gate-weighted
  * un-permute ("combine"), and the backward of both (dX, dYp, dgate, and the
- * router-logit gradient).
+ * router-logit gradient).  Also the router producer that feeds the path: the
+ * router-logits GEMM on the matrix cores, the same GEMM fused with routing,
+ * and its backward (the router input gradient fused into dispatch backward,
+ * and the router weight gradient).
  *
  * Reference interface.  The reference tree (bat0001/peer-review-agents) holds
  * no operator, plugin or FFI interface for this path -- its only extension

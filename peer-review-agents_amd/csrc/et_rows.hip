@@ -1,6 +1,7 @@
 // et_rows.hip -- the row-moving kernels of the path on gfx950: dispatch
 // (permute), combine (gate-weighted un-permute), combine backward (dYp, dgate,
-// dlogits) and dispatch backward (dX).
+// dlogits) and dispatch backward (dX, optionally with the router's input
+// gradient dlogits . W added in the same pass).
 //
 // All four are token-major: a token's slot list token_slot[token_offsets[t] ..
 // token_offsets[t+1]) is read by the waves that own the token, and whole rows
@@ -10,10 +11,11 @@
 // registers in ascending expert order without atomics.
 //
 // Vector path: rows whose byte size is a multiple of 16 move as 16-byte chunks,
-// 64 lanes x 16 B = 1 KiB per wave instruction (fully coalesced).  Dispatch and
-// combine split a row into pieces with one wave each; combine backward keeps a
-// whole row per wave so that each slot's dot product is one wave reduction.
-// Rows of other sizes take the element path.
+// 64 lanes x 16 B = 1 KiB per wave instruction (fully coalesced).  Every row
+// kernel splits a row into 1 KiB pieces with one wave each; combine backward
+// writes one partial dot product per (slot, piece), and a slot-parallel finish
+// kernel sums them in piece order into dgate and dlogits.  Rows of other sizes
+// take the element path.
 #include <algorithm>
 
 #include "et_common.hpp"
