@@ -195,8 +195,11 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
  *   x bf16 [T, d], w bf16 [E, d] (the router weight in nn.Linear layout),
  *   16-byte aligned; d a multiple of 8 below 2^22; 1 <= E <= ET_MAX_ROUTER_EXPERTS.
  * Products of bf16 values are exact in binary32; the sum over k runs in a
- * fixed order, so repeated calls give identical bits, and integer-valued
- * inputs whose partial sums stay below 2^24 give the exact integer result.
+ * fixed order, in k-steps of 16 ascending from k0(t) = (floor(t / 256) mod 4) *
+ * 64 * floor(d / 256) and wrapping to 0 (staggered so that concurrent blocks
+ * read different column ranges of X).  So repeated calls give identical bits,
+ * and integer-valued inputs whose partial sums stay below 2^24 give the exact
+ * integer result.
  * Implements the router producer that feeds the path (no reference counterpart).
  */
 int et_router_logits(const void* x, const void* w, int64_t num_tokens, int64_t d, int64_t num_experts,

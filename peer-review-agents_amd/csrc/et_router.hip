@@ -175,8 +175,10 @@ __device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], co
 
 // A block owns TOK tokens at a time and loops over token tiles (the grid is
 // capped); wave w owns tokens [t0, t0 + 32 * MT).  Every wave sums k in
-// ascending k-steps of 16, one MFMA per step, token tile and expert tile, so
-// the bits of a logit depend on d only -- not on T, E or the tiling.
+// k-steps of 16, one MFMA per step, token tile and expert tile, ascending from
+// k0(t) = (floor(t / 256) mod 4) * 64 * floor(d / 256) and wrapping to 0, so
+// the bits of a logit depend on d and floor(t / 256) mod 4 only -- not on T,
+// E or the tiling.
 template <int NT, int MW, int MT, int R, bool ROUTE>
 __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int d, int E,
@@ -202,8 +204,18 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
     const __amdgpu_buffer_rsrc_t wres =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(w), (short)0, (int)((int64_t)E * d * 2), kBufDword3);
 
+    static_assert(256 % S::TOK == 0, "a block tile lies inside one 256-token group");
     for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t t0 = (int64_t)tile * S::TOK + (int64_t)wave * (32 * MT);
+        // The k walk of token group g = t / 256 starts at k0 = (g mod 4) * 64 *
+        // floor(d / 256) and wraps.  Rows are 2d bytes apart; with d a
+        // multiple of a large power of two, blocks walking the same column
+        // range at the same time hit a subset of the HBM channels (at C3 the
+        // X stream drops from ~6.0 to ~4.7 TB/s).  Chunks past the end stay
+        // past the end, so their loads read zeros.
+        const int grp = (int)(((int64_t)tile * S::TOK) >> 8);
+        const int rot = (grp & 3) * (d / 256) * (64 / S::KC);
+        auto chunk_at = [&](int c) { return c < nchunks ? (c + rot < nchunks ? c + rot : c + rot - nchunks) : c; };
         const int64_t rows_here = max<int64_t>(0, min<int64_t>(32 * MT, (int64_t)T - t0));
         const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(x + (t0 < T ? t0 : 0) * (int64_t)d), (short)0, (int)(rows_here * d * 2),
@@ -215,7 +227,7 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             for (int i = 0; i < S::SEGS_PER_THREAD; ++i) {
                 const int seg = min(tid + i * S::THREADS, S::SEGS - 1);
                 const int e = seg / (S::KC / 8);
-                const int k = c * S::KC + (seg % (S::KC / 8)) * 8;
+                const int k = chunk_at(c) * S::KC + (seg % (S::KC / 8)) * 8;
                 const uint32_t off = k < d ? ((uint32_t)e * (uint32_t)d + (uint32_t)k) * 2u : kBufOutOfRange;
                 wr[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wres, off, 0, 0));
             }
@@ -237,7 +249,7 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             for (int m = 0; m < MT; ++m)
 #pragma unroll
                 for (int s = 0; s < S::KSTEPS; ++s) {
-                    const int k = c * S::KC + s * 16 + half * 8;
+                    const int k = chunk_at(c) * S::KC + s * 16 + half * 8;
                     const uint32_t off =
                         k < d ? (uint32_t)(m * 32 + row) * (uint32_t)d * 2u + (uint32_t)k * 2u : kBufOutOfRange;
                     a[m][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));

@@ -27,7 +27,7 @@ constexpr int kHistWaves = 16;
 constexpr int kHistThreads = kHistWaves * kWave;
 constexpr int64_t kHistBlocksFirst = 256;   // blocks of the score pass (whole grid)
 constexpr int kHistUTFirst = 8;             // tokens in flight per wave, score pass
-constexpr int64_t kHistBlocksKeys = 128;    // blocks of the key passes (whole grid)
+constexpr int64_t kHistBlocksKeys = 256;    // blocks of the key passes (whole grid)
 constexpr int kHistUTKeys = 16;             // tokens in flight per wave, key passes
 constexpr int64_t kMaxTokensPerBlock = 65535;  // LDS counts are 16-bit
 constexpr int kPitch = kWave + 1;           // LDS words per digit pair (padded)

@@ -396,7 +396,9 @@ def router_logits(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] 
     """Router logits L = X W^T in float32 from bf16 X [T, d] and W [E, d].
 
     W is the router weight in nn.Linear layout.  Binary32 accumulation in a
-    fixed order on the matrix cores: repeated calls give identical bits.
+    fixed order on the matrix cores (k-steps of 16 ascending from
+    k0 = (t // 256 % 4) * 64 * (d // 256), wrapping to 0): repeated calls give
+    identical bits.
     """
     _require(x, "x", torch.bfloat16, 2)
     dev = x.device

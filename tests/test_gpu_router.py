@@ -67,6 +67,27 @@ def test_router_logits_random_within_bound(et, dev):
     assert float((err / mass).mean()) < 4 * d ** 0.5 * 2.0 ** -24
 
 
+@pytest.mark.parametrize("T,E", [(2048, 16), (2048, 200), (66000, 128), (66000, 256)])
+def test_router_logits_k_order(et, dev, T, E):
+    """The k walk of token t starts at k0 = (floor(t / 256) mod 4) * 64 *
+    floor(d / 256) and wraps.  With d = 512, x = 2^24 at k = 0 and 1 at k = 128
+    and k = 256, and w = 1: from k0 = 128 (t / 256 = 1 mod 4) the two ones meet
+    first and the sum is 2^24 + 2; from k0 = 0, 256 or 384 each one is added to
+    2^24 and rounds away (ties to even).  Both launch shapes and both k-chunk
+    widths (E <= 128 and E > 128) give the same bits."""
+    print(f"router_logits k order T={T} E={E}", flush=True)
+    d = 512
+    x = torch.zeros(T, d, device=dev, dtype=torch.bfloat16)
+    x[:, 0] = 2.0 ** 24
+    x[:, 128] = 1.0
+    x[:, 256] = 1.0
+    w = torch.ones(E, d, device=dev, dtype=torch.bfloat16)
+    L = et.router_logits(x, w)
+    t = torch.arange(T, device=dev)
+    want = torch.where((t // 256) % 4 == 1, 2.0 ** 24 + 2, 2.0 ** 24).double()
+    assert torch.equal(L.double(), want[:, None].expand(T, E))
+
+
 def test_router_logits_full_size_c3_and_routing(et, orc, dev):
     cfg = W.CONFIGS["C3"]
     T, d, E = cfg["T"], cfg["d"], cfg["E"]
