@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_exp_nonpos.argtypes = [ctypes.c_float]
         L.oracle_sigmoid.restype = ctypes.c_float
         L.oracle_sigmoid.argtypes = [ctypes.c_float]
+        L.oracle_sigmoid_order_scan.restype = None
+        L.oracle_sigmoid_order_scan.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _p]
         L.oracle_select.restype = _i64
         L.oracle_select.argtypes = [_p, _p, _i64, _i64, _p, _p]
         L.oracle_route.restype = _i64
@@ -109,6 +111,15 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
 
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def sigmoid_order_scan(k0: int, k1: int) -> tuple:
+    """(largest deficit below the running max in order steps, smallest score
+    bits, largest score bits, negative scores) of the specified sigmoid over
+    the floats with order index in [k0, k1) (oracle_sigmoid_order_scan)."""
+    out = np.zeros(4, np.uint32)
+    lib().oracle_sigmoid_order_scan(k0, k1, out.ctypes.data)
+    return tuple(int(v) for v in out)
 
 
 def sigmoid(logits: np.ndarray) -> np.ndarray:

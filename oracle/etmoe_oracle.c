@@ -111,6 +111,34 @@ float oracle_sigmoid(float l)
     return z / (1.0f + z);
 }
 
+/* Order scan of the sigmoid: over the floats with order index k in [k0, k1)
+ * (k < 2^31: the negative floats from the most negative up to -0, as bit
+ * patterns 0xFFFFFFFF - k; k >= 2^31: +0 up to +inf, bit patterns k - 2^31),
+ * NaN logits skipped, with M(l) the running maximum of the scores so far:
+ *   out[0] = largest bits(M(l)) - bits(sigmoid(l))   (order steps below M)
+ *   out[1] = smallest score bit pattern, out[2] = largest,
+ *   out[3] = count of scores with the sign bit set.
+ * Scores are compared by bit pattern, which orders non-negative floats by
+ * value.  Test infrastructure: it measures how far the specified sigmoid is
+ * from monotone (the device's logit-domain selection bounds rely on it). */
+void oracle_sigmoid_order_scan(uint64_t k0, uint64_t k1, uint32_t* out)
+{
+    uint32_t worst = 0, lo = 0xFFFFFFFFu, hi = 0, neg = 0, m = 0;
+    int started = 0;
+    for (uint64_t k = k0; k < k1; ++k) {
+        const uint32_t bits = k < 0x80000000ull ? (uint32_t)(0xFFFFFFFFull - k) : (uint32_t)(k - 0x80000000ull);
+        const float l = u2f(bits);
+        if (l != l) continue;
+        const uint32_t b = f2u(oracle_sigmoid(l));
+        if (b & 0x80000000u) { ++neg; continue; }
+        if (b < lo) lo = b;
+        if (b > hi) hi = b;
+        if (!started || b > m) { m = b; started = 1; }
+        else if (m - b > worst) worst = m - b;
+    }
+    out[0] = worst; out[1] = lo; out[2] = hi; out[3] = neg;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Routing: threshold selection, fallback, CSR by expert, CSR by token       */
 /* ------------------------------------------------------------------------ */

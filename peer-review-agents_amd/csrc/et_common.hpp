@@ -60,11 +60,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
 // exp(x) for x <= 0: Cody-Waite reduction with n = rint(x*log2 e), ln2 split
 // into an exact high part and a low part, degree-7 Taylor polynomial of exp(r)
 // on |r| <= ln2/2 in Horner form with fma, scaled by 2^n through the exponent
-// field.  x < -87 gives 0, so no result is subnormal.
-__device__ __forceinline__ float exp_nonpos(float x)
+// field.  x < -87 gives 0, so no result is subnormal.  The special cases
+// (NaN, x < -87) are selected at the end rather than branched around: inside
+// a wave those branches diverge and cost more than the polynomial.
+__device__ __forceinline__ float exp_nonpos(float x_in)
 {
-    if (x != x) return x;
-    if (x < -87.0f) return 0.0f;
+    const bool nan = x_in != x_in;
+    const bool under = x_in < -87.0f;
+    const float x = (nan || under) ? 0.0f : x_in;
     const float log2e = 1.4426950216293335f;     // 0x3FB8AA3B
     const float ln2_hi = 0.693145751953125f;     // 0x3F317200
     const float ln2_lo = 1.428606765330187e-6f;  // 0x35BFBE8E
@@ -80,7 +83,8 @@ __device__ __forceinline__ float exp_nonpos(float x)
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
     int ni = (int)n;
-    return p * u2f((uint32_t)(ni + 127) << 23);
+    const float v = p * u2f((uint32_t)(ni + 127) << 23);
+    return nan ? x_in : (under ? 0.0f : v);
 }
 
 // sigmoid(l): l >= 0 -> 1/(1+exp(-l)); l < 0 -> exp(l)/(1+exp(l)); NaN stays NaN.

@@ -414,39 +414,53 @@ __global__ __launch_bounds__(kMaxGroupsPerTile * kWave) void route_fill_masks_ke
 #pragma unroll
             for (int u = 0; u < UT; ++u) wv[u][g] = masks[min(tb + u, t1 - 1) * nwords + wi];
         }
+        // Three passes over the UT tokens: ranks within each token (ballots),
+        // then every gate load (their list positions follow from the token
+        // counts alone), then the stores -- so a batch waits for one round
+        // trip to the gate list rather than one per token.
+        int rk[UT][GM];                                 // rank of the lane's pair within its token, -1 if none
+        int kt[UT];
+#pragma unroll
+        for (int u = 0; u < UT; ++u) {
+            int below = 0;
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                const int e = g * kWave + lane;
+                const bool bit = tb + u < t1 && g < G && e < E && ((wv[u][g] >> (lane & 31)) & 1u);
+                const uint64_t m = (uint64_t)__ballot(bit);
+                rk[u][g] = bit ? below + rank_below(m) : -1;
+                below += (int)__popcll(m);
+            }
+            kt[u] = below;
+        }
+        float gate[UT][GM];
+        {
+            int tp = tok_pos - tok_pos0;
+#pragma unroll
+            for (int u = 0; u < UT; ++u) {
+#pragma unroll
+                for (int g = 0; g < GM; ++g) gate[u][g] = gl[min(tp + max(rk[u][g], 0), 16 * E - 1)];   // the group's list
+                tp += kt[u];
+            }
+        }
 #pragma unroll
         for (int u = 0; u < UT; ++u) {
             if (tb + u >= t1) break;
             const int t = (int)(tb + u);
-            uint64_t m[GM];
-            int k = 0;
-#pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                const int e = g * kWave + lane;
-                const bool bit = g < G && e < E && ((wv[u][g] >> (lane & 31)) & 1u);
-                m[g] = (uint64_t)__ballot(bit);
-                k += (int)__popcll(m[g]);
-            }
             if (lane == 0) token_offsets[t] = tok_pos;
-            int below = 0;
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
-                if (g < G) {
-                    if ((m[g] >> lane) & 1ull) {
-                        const int rank = below + rank_below(m[g]);
-                        const int gi = min(tok_pos - tok_pos0 + rank, 16 * E - 1);   // within the group's list
-                        const float gate = gl[gi];
-                        if ((int64_t)pos[g] < cap) {
-                            sorted_token[pos[g]] = t;
-                            slot_gate[pos[g]] = gate;
-                        }
-                        if ((int64_t)tok_pos + rank < cap) token_slot[tok_pos + rank] = pos[g];
-                        ++pos[g];
+                const int rank = rk[u][g];
+                if (rank >= 0) {
+                    if ((int64_t)pos[g] < cap) {
+                        sorted_token[pos[g]] = t;
+                        slot_gate[pos[g]] = gate[u][g];
                     }
-                    below += (int)__popcll(m[g]);
+                    if ((int64_t)tok_pos + rank < cap) token_slot[tok_pos + rank] = pos[g];
+                    ++pos[g];
                 }
             }
-            tok_pos += k;
+            tok_pos += kt[u];
         }
     }
 }
@@ -482,11 +496,18 @@ int launch_route_fill_masks(const uint32_t* masks, const float* gate_ws, int T, 
     if (gpt < 1 || gpt > kMaxGroupsPerTile)
         return fail(ET_ERR_INVALID_ARGUMENT, "route_fill_masks: route groups per tile must be 1..16");
     if (NB == 0) return ET_OK;
+    // The producer's expert counts stop at 256 (4 groups of 64); a route
+    // group is 16 tokens, so one batch covers it up to 2 groups.
     const int G = (E + kWave - 1) / kWave;
-    ET_SWITCH_GROUPS(G, route_fill_masks_kernel<GM, UT><<<dim3(NB), dim3(gpt * kWave), 0, s>>>(
-                            masks, gate_ws, T, E, gpt, counts, group_counts, block_base, group_slots,
-                            block_slot_base, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
-                            cap));
+    if (G > 4) return fail(ET_ERR_INVALID_ARGUMENT, "route_fill_masks: at most 256 experts");
+#define ET_FILL_MASKS(GM_, UT_)                                                                              \
+    route_fill_masks_kernel<GM_, UT_><<<dim3(NB), dim3(gpt * kWave), 0, s>>>(                                \
+        masks, gate_ws, T, E, gpt, counts, group_counts, block_base, group_slots, block_slot_base,           \
+        expert_offsets, token_offsets, sorted_token, slot_gate, token_slot, cap)
+    if (G <= 1) ET_FILL_MASKS(1, 16);
+    else if (G <= 2) ET_FILL_MASKS(2, 16);
+    else ET_FILL_MASKS(4, 8);
+#undef ET_FILL_MASKS
     return check_launch("route_fill_masks_kernel");
 }
 

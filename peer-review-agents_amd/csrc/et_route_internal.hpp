@@ -33,11 +33,49 @@ __device__ __forceinline__ void load_thresholds(const float* __restrict__ thr, i
 // ties to the lowest expert index; lanes past E hold NaN, so an all-NaN token
 // goes to expert 0).  Returns the token's expert count (wave-uniform).  Scores
 // are sigmoids, so never negative: their bit patterns order like the values.
-template <int GM>
-__device__ __forceinline__ int select_token(const float (&lg)[GM], const float (&th)[GM], int G,
-                                            uint64_t (&m)[GM], float (&sc)[GM])
+// Logit-domain bounds of the test sigmoid(l) >= th, for one expert.  The
+// specified sigmoid is monotone up to 2 order steps: over all non-NaN floats,
+// bits(s(l)) >= bits(max_{l' <= l} s(l')) - 2, and s(l) >= +0 (exhaustive
+// check over all 2^32 floats; scores are non-negative, so their bit patterns
+// order like their values).  Hence a logit hi with bits(s(hi)) >= bits(th) + 2
+// gives s(l) >= th for every l >= hi, and a logit lo with bits(s(lo)) + 2 <
+// bits(th) gives s(l) < th for every l <= lo.  Both are found by stepping out
+// from an approximate logit of th, each candidate checked with the exact
+// sigmoid; a bound that is not found is NaN and decides nothing.  Logits
+// strictly between the bounds, and NaN logits, need the exact score.
+//   th NaN or > 1: nothing is selected (hi = NaN, lo = +inf).
+//   th <= 0:       every non-NaN logit is selected (hi = -inf, lo = NaN).
+__device__ __forceinline__ void select_bounds(float th, float& hi, float& lo)
 {
-    const int lane = lane_id();
+    const float inf = __builtin_huge_valf();
+    const float nan = __builtin_nanf("");
+    if (!(th <= 1.0f)) { hi = nan; lo = inf; return; }
+    if (th <= 0.0f) { hi = -inf; lo = nan; return; }
+    const uint32_t tb = f2u(th);
+    const float l0 = th < 1.0f ? __logf(th) - __logf(1.0f - th) : 20.0f;   // approximate logit of th
+    const float s0 = __builtin_fmaxf(__builtin_fabsf(l0) * 0x1p-18f, 0x1p-20f);
+    hi = nan;
+    float step = s0;
+    for (int it = 0; it < 24; ++it) {
+        const float h = l0 + step;
+        if (f2u(sigmoid(h)) >= tb + 2u) { hi = h; break; }
+        step *= 4.0f;
+    }
+    lo = nan;
+    step = s0;
+    for (int it = 0; it < 24; ++it) {
+        const float g = l0 - step;
+        if (f2u(sigmoid(g)) + 2u < tb) { lo = g; break; }
+        step *= 4.0f;
+    }
+}
+
+// The threshold part of the rule: scores, ballots and the expert count, with
+// no fallback (the count may be 0).
+template <int GM>
+__device__ __forceinline__ int select_scores(const float (&lg)[GM], const float (&th)[GM], int G,
+                                             uint64_t (&m)[GM], float (&sc)[GM])
+{
     int k = 0;
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
@@ -45,25 +83,41 @@ __device__ __forceinline__ int select_token(const float (&lg)[GM], const float (
         m[g] = (g < G) ? (uint64_t)__ballot(sc[g] >= th[g]) : 0ull;
         k += (int)__popcll(m[g]);
     }
-    if (k == 0) {
-        // Argmax by two DPP reductions (no LDS round trips).  Keys order the
-        // scores (all >= 0) by their bits, with NaN below every score; each
-        // lane keeps its best group, the lowest on ties.  The wave max of the
-        // keys is the best score; the wave max of ~e over the lanes holding
-        // it is the lowest expert index with that score.
-        uint32_t bk = 0u;
-        int be = lane;
+    return k;
+}
+
+// The fallback part: m = the argmax expert of the scores sc (NaN lowest, ties
+// to the lowest expert index).  Argmax by two DPP reductions (no LDS round
+// trips).  Keys order the scores (all >= 0) by their bits, with NaN below
+// every score; each lane keeps its best group, the lowest on ties.  The wave
+// max of the keys is the best score; the wave max of ~e over the lanes holding
+// it is the lowest expert index with that score.
+template <int GM>
+__device__ __forceinline__ void select_fallback(const float (&sc)[GM], int G, uint64_t (&m)[GM])
+{
+    const int lane = lane_id();
+    uint32_t bk = 0u;
+    int be = lane;
 #pragma unroll
-        for (int g = 0; g < GM; ++g) {
-            if (g < G) {
-                const uint32_t key = (sc[g] != sc[g]) ? 0u : f2u(sc[g]) + 1u;
-                if (key > bk) { bk = key; be = g * kWave + lane; }
-            }
+    for (int g = 0; g < GM; ++g) {
+        if (g < G) {
+            const uint32_t key = (sc[g] != sc[g]) ? 0u : f2u(sc[g]) + 1u;
+            if (key > bk) { bk = key; be = g * kWave + lane; }
         }
-        const uint32_t top = wave_max_u32_dpp(bk);
-        be = (int)~wave_max_u32_dpp(bk == top ? ~(uint32_t)be : 0u);
+    }
+    const uint32_t top = wave_max_u32_dpp(bk);
+    be = (int)~wave_max_u32_dpp(bk == top ? ~(uint32_t)be : 0u);
 #pragma unroll
-        for (int g = 0; g < GM; ++g) m[g] = (g == (be >> 6)) ? (1ull << (be & (kWave - 1))) : 0ull;
+    for (int g = 0; g < GM; ++g) m[g] = (g == (be >> 6)) ? (1ull << (be & (kWave - 1))) : 0ull;
+}
+
+template <int GM>
+__device__ __forceinline__ int select_token(const float (&lg)[GM], const float (&th)[GM], int G,
+                                            uint64_t (&m)[GM], float (&sc)[GM])
+{
+    int k = select_scores<GM>(lg, th, G, m, sc);
+    if (k == 0) {
+        select_fallback<GM>(sc, G, m);
         k = 1;
     }
     return k;

@@ -63,23 +63,33 @@ struct RouteEpilogue {
 
 // Routing epilogue of one producer tile.  The wave's logits pass through a
 // wave-private LDS buffer, 16 tokens at a time, and are then walked token by
-// token with lane = expert, through the same select_token as et_route (so the
-// selection, gates and argmax fallback are those of et_route by construction).
+// token with lane = expert.  Selection is decided in the logit domain by the
+// per-expert bounds of select_bounds, with the exact score only for logits
+// between the bounds (or NaN); tokens with no expert take select_fallback on
+// exact scores.  So the selection, gates and argmax fallback are those of
+// et_route (select_token) bit for bit, with far fewer sigmoids: gates are
+// computed only for the routed pairs, after each 16-token group.
 // acc[m][n][j] is the logit of token t0 + 32 m + r, r = 8 (j / 4) +
-// 4 (lane / 32) + j % 4, expert 32 n + lane % 32.  Ends with a barrier.
+// 4 (lane / 32) + j % 4, expert 32 n + lane % 32.  The waves run through it
+// independently; the tile sums at the end take two block barriers (`red`
+// aliases the W buffer, which every wave has finished reading once the K
+// loop's last barrier has passed).
 template <int NT, int MW, int MT>
 __device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], const RouteEpilogue& ro,
                                                float* rbuf, int* red, int tile, int wave, int64_t t0, int T, int E)
 {
     constexpr int P = NT * 32 + 8;              // LDS row pitch (floats): both halves' writes on distinct banks
     constexpr int GM = (NT * 32 + kWave - 1) / kWave;
+    constexpr int DUMMY = 16 * P - 1;           // padding of the last row: never a logit, never a list entry
     const int lane = lane_id();
     const int half = lane >> 5;
     const int row = lane & 31;
     const int G = (E + kWave - 1) / kWave;
     const int nwords = (E + 31) / 32;
-    float th[GM];
+    float th[GM], hi[GM], lo[GM];
     load_thresholds<GM>(ro.thr, E, G, th);
+#pragma unroll
+    for (int g = 0; g < GM; ++g) select_bounds(th[g], hi[g], lo[g]);
     int wcnt[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) wcnt[g] = 0;
@@ -97,47 +107,93 @@ __device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], co
                     const int u = 8 * (jj / 4) + 4 * half + (j % 4);
                     rbuf[u * P + n * 32 + row] = acc[m][n][j];
                 }
-            __syncthreads();
+            // rbuf is private to this wave and a wave's LDS operations run in
+            // issue order, so the fences only have to keep the compiler from
+            // moving these accesses across each other.
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             const int64_t tg = t0 + m * 32 + 16 * hh;     // first token of the route group
             const int64_t q = tg / 16;
-            float* gl = ro.gate_ws + q * 16 * (int64_t)E;
+            const int nu = (int)std::min<int64_t>(16, std::max<int64_t>(0, (int64_t)T - tg));
+            // Stores go through range-checked buffer descriptors: a lane with
+            // nothing to store gives an out-of-range offset and its store is
+            // dropped, with no branch on the exec mask.
+            const __amdgpu_buffer_rsrc_t gres =
+                __builtin_amdgcn_make_buffer_rsrc(ro.gate_ws + q * 16 * (int64_t)E, (short)0, 16 * E * 4, kBufDword3);
+            const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
+                ro.masks + (tg < T ? tg : 0) * nwords, (short)0, nu * nwords * 4, kBufDword3);
             int cnt[GM];
 #pragma unroll
             for (int g = 0; g < GM; ++g) cnt[g] = 0;
             int lp = 0;
-            const int nu = (int)std::min<int64_t>(16, std::max<int64_t>(0, (int64_t)T - tg));
-#pragma unroll 4
-            for (int u = 0; u < nu; ++u) {
-                const int64_t t = tg + u;
-                float lg[GM];
+            // Tokens in batches of UB (selections within a batch are
+            // independent); the fallback and the outputs follow in token order.
+            // The routed pairs' logits are listed in rbuf at their gate
+            // positions: the entries of tokens < u + 1 lie below (u + 1) * E <=
+            // (u + 1) * P, i.e. in rows already read.
+            constexpr int UB = 8 / GM;
+#pragma unroll 1
+            for (int ub = 0; ub < 16; ub += UB) {
+                float lg[UB][GM];
+                uint64_t mm[UB][GM];
+                int kk[UB];
 #pragma unroll
-                for (int g = 0; g < GM; ++g) {
-                    const int e = g * kWave + lane;
-                    lg[g] = (g < G && e < E) ? rbuf[u * P + e] : __builtin_nanf("");
-                }
-                uint64_t mm[GM];
-                float sc[GM];
-                const int k = select_token<GM>(lg, th, G, mm, sc);
-                uint32_t word = 0u;                     // lane i < nwords writes mask word i
+                for (int i = 0; i < UB; ++i) {
+                    const int u = ub + i;
+                    kk[i] = 0;
 #pragma unroll
-                for (int g = 0; g < GM; ++g) {
-                    if (lane == 2 * g) word = (uint32_t)mm[g];
-                    if (lane == 2 * g + 1) word = (uint32_t)(mm[g] >> 32);
-                }
-                if (lane < nwords) ro.masks[t * nwords + lane] = word;
-                int below = 0;
-#pragma unroll
-                for (int g = 0; g < GM; ++g) {
-                    if (g < G) {
-                        if ((mm[g] >> lane) & 1ull) {
-                            const int gi = lp + below + rank_below(mm[g]);
-                            if (gi < 16 * E) gl[gi] = sc[g];
-                            ++cnt[g];
-                        }
-                        below += (int)__popcll(mm[g]);
+                    for (int g = 0; g < GM; ++g) {
+                        const int e = g * kWave + lane;
+                        const float v = rbuf[u * P + min(e, NT * 32 - 1)];   // in bounds for every lane
+                        const bool valid = u < nu && g < G && e < E;
+                        lg[i][g] = valid ? v : __builtin_nanf("");
+                        const bool sure = lg[i][g] >= hi[g];
+                        const bool amb = valid && !sure && !(lg[i][g] <= lo[g]);
+                        bool sel = sure;
+                        if (__ballot(amb) != 0ull) sel = amb ? sigmoid(lg[i][g]) >= th[g] : sure;
+                        mm[i][g] = (uint64_t)__ballot(sel);
+                        kk[i] += (int)__popcll(mm[i][g]);
                     }
                 }
-                lp += k;
+#pragma unroll
+                for (int i = 0; i < UB; ++i) {
+                    const int u = ub + i;
+                    if (u < nu) {
+                        if (kk[i] == 0) {
+                            float sc[GM];
+#pragma unroll
+                            for (int g = 0; g < GM; ++g) sc[g] = sigmoid(lg[i][g]);
+                            select_fallback<GM>(sc, G, mm[i]);
+                            kk[i] = 1;
+                        }
+                        uint32_t word = 0u;                     // lane i < nwords writes mask word i
+#pragma unroll
+                        for (int g = 0; g < GM; ++g) {
+                            word = lane == 2 * g ? (uint32_t)mm[i][g] : word;
+                            word = lane == 2 * g + 1 ? (uint32_t)(mm[i][g] >> 32) : word;
+                        }
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            word, mres, lane < nwords ? (uint32_t)(u * nwords + lane) * 4u : kBufOutOfRange, 0, 0);
+                        int below = 0;
+#pragma unroll
+                        for (int g = 0; g < GM; ++g) {
+                            if (g < G) {
+                                const bool sel = (mm[i][g] >> lane) & 1ull;
+                                const int gi = lp + below + rank_below(mm[i][g]);   // < 16 E: the group's pairs
+                                rbuf[sel ? gi : DUMMY] = lg[i][g];
+                                cnt[g] += sel ? 1 : 0;
+                                below += (int)__popcll(mm[i][g]);
+                            }
+                        }
+                        lp += kk[i];
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            // gates of the group's routed pairs, in list order
+            for (int j0 = 0; j0 < lp; j0 += kWave) {
+                const int j = j0 + lane;
+                const float gate = sigmoid(rbuf[min(j, DUMMY)]);
+                __builtin_amdgcn_raw_buffer_store_b32(f2u(gate), gres, j < lp ? (uint32_t)j * 4u : kBufOutOfRange, 0, 0);
             }
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
@@ -147,7 +203,7 @@ __device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], co
             }
             if (lane == 0) ro.group_slots[q] = lp;
             wslots += lp;
-            __syncthreads();                            // rbuf is rewritten by the next group
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // rbuf is rewritten by the next group
         }
     }
     // tile sums through LDS
@@ -283,19 +339,25 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             load_x(c + S::PF, xr[(r + S::PF) % R]);
             __builtin_amdgcn_sched_barrier(0);
             const uint16_t* wb = wl[r & 1];
-#pragma unroll
-            for (int s = 0; s < S::KSTEPS; ++s) {
-                u32x4_t bf[NT];
+            u32x4_t bf[2][NT];
+            auto rdb = [&](int s, int b) {
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
-                    bf[n] = *reinterpret_cast<const u32x4_t*>(&wb[(n * 32 + row) * S::PITCH + s * 16 + half * 8]);
+                    bf[b][n] = *reinterpret_cast<const u32x4_t*>(&wb[(n * 32 + row) * S::PITCH + s * 16 + half * 8]);
+            };
+            rdb(0, 0);
+#pragma unroll
+            for (int s = 0; s < S::KSTEPS; ++s) {
+                if (s + 1 < S::KSTEPS) rdb(s + 1, (s + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
 #pragma unroll
                     for (int m = 0; m < MT; ++m)
                         acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            __builtin_bit_cast(bf16x8_t, xr[r][m][s]), __builtin_bit_cast(bf16x8_t, bf[n]), acc[m][n],
-                            0, 0, 0);
+                            __builtin_bit_cast(bf16x8_t, xr[r][m][s]), __builtin_bit_cast(bf16x8_t, bf[s & 1][n]),
+                            acc[m][n], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
             store_w((r + 1) & 1, wreg[(r + 1) & 1]);
             __syncthreads();

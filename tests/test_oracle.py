@@ -69,6 +69,32 @@ def test_sigmoid_within_two_ulp_and_monotone(orc):
     assert np.all(np.diff(got[order]) >= 0)
 
 
+def test_sigmoid_is_monotone_up_to_two_order_steps_over_all_floats(orc):
+    """Exhaustive over all 2^32 bit patterns (NaN logits skipped): the
+    specified sigmoid never returns a negative score, and each score is at most
+    2 order steps (bit patterns of non-negative floats) below the running
+    maximum of the scores of all smaller logits.  The device's logit-domain
+    selection bounds (a logit at or above hi, with bits(s(hi)) >= bits(thr) + 2,
+    is selected; at or below lo, with bits(s(lo)) + 2 < bits(thr), is not) are
+    sound exactly because of this bound.  A plain step too far (3) fails."""
+    from concurrent.futures import ThreadPoolExecutor
+    n = 16
+    edges = [(i << 32) // n for i in range(n + 1)]
+    with ThreadPoolExecutor(max_workers=8) as ex:   # the C scan releases the GIL
+        parts = list(ex.map(lambda i: orc.sigmoid_order_scan(edges[i], edges[i + 1]), range(n)))
+    worst, prefix_max = 0, None
+    for deficit, lo, hi, neg in parts:
+        assert neg == 0
+        worst = max(worst, deficit)
+        if prefix_max is not None and prefix_max > lo:
+            worst = max(worst, prefix_max - lo)      # earlier ranges' maximum against this range
+        prefix_max = hi if prefix_max is None else max(prefix_max, hi)
+    assert worst == 2
+    # the scan itself: on a range known to dip (just below l = -0.25) it reports the dip
+    k = 0xFFFFFFFF - 0xBE80_0000                      # order index of -0.25
+    assert orc.sigmoid_order_scan(k - (1 << 20), k + (1 << 20))[0] >= 1
+
+
 def test_sigmoid_special_values(orc):
     v = orc.sigmoid(np.float32([0.0, -0.0, np.inf, -np.inf, 100.0, -100.0, 20.0]))
     assert v[0] == 0.5 and v[1] == 0.5
