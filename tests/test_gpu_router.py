@@ -195,6 +195,53 @@ def test_router_route_argmax_fallback_and_nonfinite(et, dev):
         _assert_plans_identical(et.router_route(x, w, thr), et.route(L, thr))
 
 
+def test_router_route_logits_at_the_threshold(et, orc, dev):
+    """The fused epilogue decides most pairs in the logit domain (per-expert
+    bounds around the logit of the threshold) and takes the exact score only
+    between the bounds.  Here every logit sits within a few float steps of its
+    expert's threshold logit l0 (thr = sigmoid(l0) as the oracle computes it,
+    or one step above or below), so the exact path decides most pairs; other
+    experts carry threshold values the bounds handle specially (<= 0, -0, 1,
+    > 1, NaN, subnormal, the float below 1).  Logits are built exactly as
+    a + b 2^-8 + c 2^-16 from three bf16 terms against a W holding 1, 2^-8 and
+    2^-16.  Fused routing must equal router_logits -> route bit for bit."""
+    E, T = 64, 4096
+    d = 3 * E + 8
+    rng = np.random.default_rng(12)
+    l0 = (rng.standard_normal(E) * 3).astype(np.float32)
+    thr = orc.sigmoid(l0).copy()
+    thr[1::3] = np.nextafter(thr[1::3], np.float32(np.inf))
+    thr[2::3] = np.nextafter(thr[2::3], np.float32(-np.inf))
+    special = [0.0, -0.0, -1.0, 1.0, 1.5, np.nan, 1e-45, np.nextafter(np.float32(1), np.float32(0)), 0.5, 3e-39]
+    thr[-len(special):] = np.float32(special)
+    # per token, each expert's logit = l0 moved by a few float steps
+    steps = rng.integers(-40, 41, size=(T, E))
+    target = l0[None, :].repeat(T, 0)
+    for k in range(1, 41):                         # nextafter, k steps either way
+        up = steps >= k
+        dn = steps <= -k
+        target[up] = np.nextafter(target[up], np.float32(np.inf))
+        target[dn] = np.nextafter(target[dn], np.float32(-np.inf))
+    a = orc.bf16_to_f32(orc.f32_to_bf16(target))
+    r1 = (target - a) * np.float32(256)
+    b = orc.bf16_to_f32(orc.f32_to_bf16(r1))
+    c = orc.bf16_to_f32(orc.f32_to_bf16((r1 - b) * np.float32(256)))
+    x = np.zeros((T, d), np.float32)
+    w = np.zeros((E, d), np.float32)
+    e = np.arange(E)
+    x[:, 3 * e], x[:, 3 * e + 1], x[:, 3 * e + 2] = a, b, c
+    w[e, 3 * e], w[e, 3 * e + 1], w[e, 3 * e + 2] = 1.0, 2.0 ** -8, 2.0 ** -16
+    xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    wb = torch.from_numpy(w).to(dev).to(torch.bfloat16)
+    thr_d = torch.from_numpy(thr).to(dev)
+    L = et.router_logits(xb, wb)
+    near = (L - torch.from_numpy(l0).to(dev)).abs() <= 64 * torch.from_numpy(np.spacing(np.abs(l0))).to(dev)
+    assert float(near[:, :-len(special)].float().mean()) > 0.99    # the logits really sit at the thresholds
+    want = et.route(L, thr_d)
+    _assert_plans_identical(et.router_route(xb, wb, thr_d), want)
+    assert_route_equal(want, orc.route(host(L), thr))
+
+
 def test_router_route_explicit_and_undersized_capacity(et, dev):
     T, d, E = 3000, 256, 64
     x, w = _router_case(dev, T, d, E, 9, 0.9)
