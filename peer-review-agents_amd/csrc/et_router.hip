@@ -394,15 +394,15 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
     }
 }
 
-// X ring length: 12-16 KiB of X in flight per wave.
-template <int NT, int MT> constexpr int kRouterRing = (NT <= 4 ? 4 : 8) / MT;
+// X ring length: 8-16 KiB of X in flight per wave (with 8 expert tiles and
+// two token tiles the accumulators alone take 256 registers).
+template <int NT, int MT> constexpr int kRouterRing = NT <= 4 ? 4 / MT : 4;
 
 template <int NT, int MW, int MT, bool ROUTE>
 static void launch_router(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* w, int64_t T, int64_t d,
                           int64_t E, float* logits, const RouteEpilogue& ro)
 {
-    constexpr int MTE = NT == 8 ? 1 : MT;       // two token tiles of 8 expert tiles do not fit the registers
-    router_logits_kernel<NT, MW, MTE, kRouterRing<NT, MTE>, ROUTE>
+    router_logits_kernel<NT, MW, MT, kRouterRing<NT, MT>, ROUTE>
         <<<grid, dim3(MW * kWave), 0, s>>>(x, w, (int)T, (int)d, (int)E, logits, ro);
 }
 
@@ -416,12 +416,11 @@ struct RouterLaunch {
 };
 constexpr int64_t kRouterMaxBlocks = 2048;
 
-static RouterLaunch router_launch(int64_t T, int nt)
+static RouterLaunch router_launch(int64_t T)
 {
     RouterLaunch L{2, 1};
     if (T >= 256 * 256) L = {4, 2};
     else if (T >= 256 * 128) L = {2, 2};
-    if (nt > 4) L.mt = 1;
     return L;
 }
 
@@ -466,7 +465,7 @@ extern "C" int et_router_logits(const void* x, const void* w, int64_t T, int64_t
         return fail(ET_ERR_INVALID_ARGUMENT, "et_router_logits: x and w must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int nt = (int)((E + 31) / 32);
-    const RouterLaunch L = router_launch(T, nt);
+    const RouterLaunch L = router_launch(T);
     const int64_t ntiles = (T + 32 * L.mw * L.mt - 1) / (32 * L.mw * L.mt);
     const dim3 grid((unsigned)std::min<int64_t>(ntiles, kRouterMaxBlocks));
     const uint16_t* xp = static_cast<const uint16_t*>(x);
@@ -525,7 +524,7 @@ RouterRouteWs router_route_ws(void* base, int64_t T, int64_t E, const RouterLaun
 extern "C" size_t et_router_route_workspace_bytes(int64_t num_tokens, int64_t num_experts)
 {
     if (num_tokens < 0 || num_experts < 1 || num_experts > ET_MAX_ROUTER_EXPERTS) return 0;
-    const RouterLaunch L = router_launch(num_tokens, (int)((num_experts + 31) / 32));
+    const RouterLaunch L = router_launch(num_tokens);
     return router_route_ws(nullptr, num_tokens, num_experts, L).bytes;
 }
 
@@ -551,7 +550,7 @@ extern "C" int et_router_route(const void* x, const void* w, const float* thr, i
     if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
         return fail(ET_ERR_INVALID_ARGUMENT, "et_router_route: x and w must be 16-byte aligned");
     const int nt = (int)((E + 31) / 32);
-    const RouterLaunch L = router_launch(T, nt);
+    const RouterLaunch L = router_launch(T);
     const RouterRouteWs ws = router_route_ws(workspace, T, E, L);
     if (workspace_bytes < ws.bytes)
         return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_router_route: workspace needs " + std::to_string(ws.bytes) +
