@@ -10,7 +10,9 @@
  * router-logit gradient).  Also the router producer that feeds the path: the
  * router-logits GEMM on the matrix cores, the same GEMM fused with routing,
  * and its backward (the router input gradient fused into dispatch backward,
- * and the router weight gradient).
+ * and the router weight gradient).  And the consumer of the dispatch: the
+ * expert grouped GEMM over the CSR slot blocks, with the dispatch gather
+ * fused into its operand load.
  *
  * Reference interface.  The reference tree (bat0001/peer-review-agents) holds
  * no operator, plugin or FFI interface for this path -- its only extension
@@ -53,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 3
+#define ET_ABI_VERSION 4
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -242,6 +244,33 @@ int et_router_route(const void* x, const void* w, const float* thr, int64_t num_
                     int64_t num_experts, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
                     int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
                     float* logits, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Expert grouped GEMM over the routing CSR (the expert FFN's projections):
+ *   c[s, n] = sum_k a[row(s), k] * w[e(s), n, k]   (bf16 operands, binary32
+ *                                                   accumulation, bf16 out)
+ * for every slot s below min(expert_offsets[E], slot_capacity), e(s) the
+ * expert whose block [expert_offsets[e], expert_offsets[e + 1]) holds s.
+ *   sorted_token != NULL (gather mode): row(s) = sorted_token[s] and a is the
+ *       token matrix X bf16 [a_rows = T, K] -- the dispatch fused into the
+ *       operand load, so Xp is never written;
+ *   sorted_token == NULL: row(s) = s and a is slot-major bf16
+ *       [slot_capacity, K] (a_rows is ignored).
+ *   w bf16 [E, N, K]: expert e's weight in nn.Linear layout (row n = output
+ *       feature n); c bf16 [slot_capacity, N].
+ * K a multiple of 8 below 2^22, N a multiple of 8, N*K*2 below 2^31 bytes;
+ * in gather mode a_rows*K*2 below 2^31 bytes.  a and w 16-byte aligned, c
+ * 8-byte aligned.  Rows of c past the routed slots are left as they were.
+ * Every output sums its k-steps of 16 in ascending k (each k-step inside one
+ * MFMA), so the gather and slot-major modes give identical bits, repeated
+ * calls give identical bits, and integer-valued inputs whose partial sums stay
+ * below 2^24 give the exact result rounded once to bf16.
+ * Implements the expert grouped GEMM that consumes the dispatch (no reference
+ * counterpart).
+ */
+int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
+                   const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
+                   int64_t slot_capacity, void* c, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,7 @@ from .expert_threshold import (  # noqa: F401
     dispatch,
     dispatch_autograd,
     dispatch_backward,
+    expert_gemm,
     route,
     route_workspace_bytes,
     router_logits,

@@ -59,6 +59,7 @@ _SIGNATURES = {
     "et_dispatch_bwd_router": (_int, [_p, _p, _p, _i64, _i64, _int, _i64, _p, _p, _p, _i64, _p, _p, _p, _sz, _p]),
     "et_router_wgrad_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "et_router_wgrad": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _sz, _p]),
+    "et_expert_gemm": (_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
 }
 
 _lib = None

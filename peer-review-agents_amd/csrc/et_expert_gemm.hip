@@ -1,0 +1,387 @@
+// et_expert_gemm.hip -- the expert grouped GEMM over the routing CSR (gfx950):
+//
+//   C[s, n] = sum_k A[row(s), k] * W[e(s), n, k]     bf16 operands, binary32
+//                                                     accumulation, bf16 out
+//
+// for every slot s below min(S, slot_capacity), where e(s) is the expert whose
+// slot block [expert_offsets[e], expert_offsets[e + 1]) holds s, and
+// row(s) = sorted_token[s] in gather mode (the dispatch is fused into the
+// operand load: A is X [T, K] and Xp is never written) or row(s) = s (A is a
+// slot-major buffer [cap, K]).  W [E, N, K] holds each expert's weight in
+// nn.Linear layout (row n of expert e is output feature n).
+//
+// Tiling.  A block of 4 waves owns 256 slots x 256 output features of one
+// expert; wave (wm, wn) owns 128 x 128 of it, 4 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16.  K advances in chunks of 64 through two LDS stages
+// filled by gfx950's direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds):
+// no staging registers, and chunk c + 1 streams in while chunk c is
+// multiplied.  One direct load fills 1 KiB of LDS, lane i's 16 bytes at 16 i;
+// it is given 8 operand rows x 128 contiguous bytes (a whole cache line per
+// row: streaming through L2 into LDS runs ~45% faster this way than with 32
+// rows x 32 bytes per instruction, the MFMA fragment's own shape).  So a stage
+// holds each operand row-major, 128 bytes (64 k) per row, and the 16-byte
+// segment s of row R sits at slot s ^ key(R), key(R) = (R & 7) ^ ((R >> 3) & 1):
+// the fragment reads (lane l: row l % 32, segment 2 * kstep + l / 32) then hit
+// 16 distinct slots of every 256-byte bank window, with no bank conflicts.
+//
+// MFMA 32x32x16 bf16 operand layout (checked on the device by the router
+// kernels): lane l holds A row l % 32 and B column l % 32 at k = 8 (l / 32) + i;
+// C column l % 32, acc[j] at row 8 (j / 4) + 4 (l / 32) + j % 4.  The product
+// is issued as mfma(W fragment, X fragment) so that C's columns are slots and
+// its rows output features: each lane then holds 4 consecutive features of
+// one slot per j / 4, stored as one 8-byte write.
+//
+// Order of the sum.  Every output sums its k-steps of 16 in ascending k, each
+// k-step inside one MFMA; so results depend on K only, not on the tile, the
+// expert or the mode, and the gather and slot-major modes give identical bits.
+//
+// Schedule.  The grid is persistent (a multiple of 8 blocks, at most one per
+// CU).  Each block computes the per-expert tile prefix once, then walks its
+// tiles.  The 8 XCDs take blocks in turn (block b runs on XCD b % 8), so XCD
+// x is given the contiguous range of tiles [x * per, (x + 1) * per); inside an
+// expert, tiles are ordered in groups of 8 slot tiles x every feature tile, so
+// the ~32 blocks running together on one XCD share 8 A tiles and 4 W tiles
+// through that XCD's L2.
+#include <algorithm>
+
+#include "et_common.hpp"
+
+namespace et {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_t;
+
+// Word 3 of a gfx9 buffer descriptor for raw (untyped, stride 0) access.
+constexpr int kBufDword3 = 0x00020000;
+// A byte offset past every descriptor's num_records (all < 2^31): loads return
+// 0 and stores are dropped.
+constexpr uint32_t kOOR = 0x80000000u;
+
+constexpr int kBM = 256;          // slots per tile
+constexpr int kBN = 256;          // output features per tile
+constexpr int kKC = 64;           // k per chunk (four k-steps of 16): 128 bytes of a row
+constexpr int kThreads = 256;
+constexpr int kGroupM = 8;        // slot tiles per group in the tile order
+constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
+constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
+
+struct GemmArgs {
+    const uint16_t* a;              // gather: X [a_rows, K]; else A [cap, K]
+    const int32_t* sorted_token;    // [cap] (gather only)
+    const uint16_t* w;              // [E, N, K]
+    const int32_t* expert_offsets;  // [E + 1]
+    uint16_t* c;                    // [cap, N]
+    int64_t a_rows;
+    int64_t cap;
+    int K, N, E;
+};
+
+// One direct-to-LDS load: this lane's 16 bytes at byte offset voff + soff of
+// the buffer land at LDS address lds + 16 * lane (soff and lds are
+// wave-uniform; lds goes in M0).  Every offset this file passes keeps
+// voff + soff inside the operand row that voff names, or marks voff out of
+// range, so the access is in bounds whether or not the range check counts
+// soff.
+// Written as inline assembly so that the compiler does not treat the load as
+// an LDS store: it would otherwise wait for every such load in flight before
+// each LDS read (a full drain of the ring).  The s_nop covers the one wait
+// state an LDS DMA needs after M0 is written.
+__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t res, uint32_t voff, uint32_t soff, uint32_t lds)
+{
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(res), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are in flight,
+// then meet the other waves.  The direct-to-LDS loads count in vmcnt and are
+// in LDS once it has dropped, so after the barrier every wave's loads of the
+// chunk are visible.  The memory clobber and the scheduling barriers keep the
+// LDS reads after this point.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool GATHER>
+__global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
+{
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kStage];
+    __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
+
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int E = g.E, K = g.K, N = g.N;
+
+    if (wave == 0) {
+        int carry = 0;
+        for (int e0 = 0; e0 < E; e0 += kWave) {
+            const int e = e0 + lane;
+            int n = 0;
+            if (e < E) {
+                const int64_t lo = min<int64_t>(g.expert_offsets[e], g.cap);
+                const int64_t hi = min<int64_t>(g.expert_offsets[e + 1], g.cap);
+                n = (int)((max<int64_t>(0, hi - lo) + kBM - 1) / kBM);
+            }
+            const int inc = wave_incl_scan(n) + carry;
+            if (e < E) ptile[e + 1] = inc;
+            carry = __shfl(inc, kWave - 1, kWave);
+        }
+        if (lane == 0) ptile[0] = 0;
+    }
+    __syncthreads();
+
+    const int nN = (N + kBN - 1) / kBN;
+    const int Q = ptile[E] * nN;
+    const int per = (Q + 7) / 8;
+    const int nloc = (int)(gridDim.x / 8);
+    const int xcd = (int)(blockIdx.x & 7);
+    const int r32 = lane & 31;
+    const int kh = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nk = (K + kKC - 1) / kKC;
+
+    for (int l = (int)(blockIdx.x >> 3); l < per; l += nloc) {
+        const int q = xcd * per + l;
+        if (q >= Q) break;
+        // the tile's expert: the last e with ptile[e] <= q / nN
+        const int v = q / nN;
+        int lo = 0, hi = E;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (ptile[mid] <= v) lo = mid;
+            else hi = mid;
+        }
+        const int e = lo;
+        const int mte = ptile[e + 1] - ptile[e];
+        const int qq = q - ptile[e] * nN;
+        const int grp = qq / (kGroupM * nN);
+        const int gm = min(kGroupM, mte - grp * kGroupM);
+        const int idx = qq - grp * kGroupM * nN;
+        const int mt = grp * kGroupM + idx % gm;
+        const int nt = idx / gm;
+        const int64_t s0 = (int64_t)g.expert_offsets[e] + (int64_t)mt * kBM;
+        const int64_t rend = min<int64_t>(g.expert_offsets[e + 1], g.cap);
+        const int rows = (int)min<int64_t>(kBM, rend - s0);
+        const int n0 = nt * kBN;
+
+        // Direct loads of a chunk: wave w fills row groups 8 w + i (i < 8) of
+        // A and of W, rows R = 64 w + 8 i + lane / 8 of the tile; lane puts
+        // segment seg = (lane % 8) ^ key(R) of its row at slot lane % 8.
+        // key(R) = (lane / 8) ^ (i & 1).  Rows past the tile's slots repeat
+        // its last slot (their outputs are not stored); features past N and
+        // invalid tokens read 0 (offset marked out of range).
+        const __amdgpu_buffer_rsrc_t ares =
+            GATHER ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a), (short)0, (int)(g.a_rows * K * 2),
+                                                       kBufDword3)
+                   : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a + s0 * K), (short)0, rows * K * 2,
+                                                       kBufDword3);
+        const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(g.w + (int64_t)e * N * K), (short)0, N * K * 2, kBufDword3);
+        uint32_t aoff[8], boff[8];
+        int segk[2];              // first k of this lane's segment, by i & 1
+#pragma unroll
+        for (int p = 0; p < 2; ++p) segk[p] = (((lane & 7) ^ (lane >> 3) ^ p)) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int R = 64 * wave + 8 * i + (lane >> 3);
+            const uint32_t seg = (uint32_t)segk[i & 1] * 2u;
+            const int row = min(R, rows - 1);
+            if constexpr (GATHER) {
+                const int tok = g.sorted_token[s0 + row];
+                aoff[i] = (uint32_t)tok < (uint32_t)g.a_rows ? (uint32_t)tok * (uint32_t)K * 2u + seg : kOOR;
+            } else {
+                aoff[i] = (uint32_t)row * (uint32_t)K * 2u + seg;
+            }
+            const int n = n0 + R;
+            boff[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
+        }
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
+        // chunk c -> stage c & 1; the chunk's column offset c * 128 bytes
+        // goes in the scalar offset.  A chunk that runs past K masks the
+        // segments at or past K (K is a multiple of 8, so a segment is all
+        // in or all out).
+        auto issue = [&](int c) {
+            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u;
+            const uint32_t soff = (uint32_t)c * 128u;
+            if ((c + 1) * kKC <= K) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    dma_b128(ares, aoff[i], soff, sb + i * 1024);
+                    dma_b128(wres, boff[i], soff, sb + kHalf + i * 1024);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t kmask = c * kKC + segk[i & 1] < K ? 0u : kOOR;
+                    dma_b128(ares, aoff[i] | kmask, soff, sb + i * 1024);
+                    dma_b128(wres, boff[i] | kmask, soff, sb + kHalf + i * 1024);
+                }
+            }
+        };
+
+        f32x16_t acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+
+        // Fragment of tile t (32 rows), k-step ks: lane l reads row R = 32 t +
+        // l % 32, segment 2 ks + l / 32, at 1024 (R / 8) + 128 (R % 8) +
+        // 16 ((2 ks + l / 32) ^ key(R)); key(R) = (l % 8) ^ ((l / 8) & 1).
+        const int fkey = (lane & 7) ^ ((lane >> 3) & 1);
+        const int flane = ((lane & 31) >> 3) * 1024 + (lane & 7) * 128;
+        const unsigned char* const abase = smem + wm * 16384 + flane;
+        const unsigned char* const bbase = smem + kHalf + wn * 16384 + flane;
+        u32x4_t f[2][2][4];       // [buffer][A, W][tile]
+        auto read_frags = [&](int c, int ks, u32x4_t (&fr)[2][4]) {
+            const int off = (c & 1) * kStage + (((2 * ks + (lane >> 5)) ^ fkey) << 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) fr[0][t] = *reinterpret_cast<const u32x4_t*>(abase + off + t * 4096);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) fr[1][t] = *reinterpret_cast<const u32x4_t*>(bbase + off + t * 4096);
+        };
+        auto mfmas = [&](const u32x4_t (&fr)[2][4]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fr[1][j]),
+                                                                        __builtin_bit_cast(bf16x8_t, fr[0][i]),
+                                                                        acc[i][j], 0, 0, 0);
+        };
+
+        // Every wave has finished reading the previous tile's stages (its
+        // last fragment reads were consumed by its MFMAs).  Only the previous
+        // tile's stores can be in flight; the first wait below counts them
+        // with the loads, since vmcnt retires in issue order.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        issue(0);
+        dma_wait_barrier<0>();
+        if (nk > 1) issue(1);
+        read_frags(0, 0, f[0]);
+        // Step c (chunk c in stage c & 1, chunk c + 1 streaming into the
+        // other): k-steps 0..2 read the next k-step's fragments while their
+        // own MFMAs issue.  Before the last k-step's MFMAs every wave waits
+        // for its fragment reads and for chunk c + 1, then meets the others:
+        // from there chunk c + 1 is visible, nobody reads chunk c any more,
+        // so chunk c + 2 may refill its stage, and chunk c + 1's first
+        // fragments load under the last k-step's MFMAs.
+        for (int c = 0; c < nk; ++c) {
+            read_frags(c, 1, f[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(c, 2, f[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(c, 3, f[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 < nk) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                dma_wait_barrier<0>();
+                if (c + 2 < nk) issue(c + 2);
+                read_frags(c + 1, 0, f[0]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // Epilogue: lane l holds slot (wm * 4 + i) * 32 + l % 32 and features
+        // (wn * 4 + j) * 32 + 8 (r / 4) + 4 (l / 32) + 0..3 in acc[i][j][4 (r / 4) ..].
+        // Range-checked stores: rows past the tile's slots and features past N
+        // are given an out-of-range offset and dropped.
+        const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * N, (short)0, rows * N * 2,
+                                                                               kBufDword3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = (wm * 4 + i) * 32 + r32;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = n0 + (wn * 4 + j) * 32 + 8 * r + 4 * kh;
+                    const u32x2_t val = {pack_bf16x2(acc[i][j][4 * r], acc[i][j][4 * r + 1]),
+                                         pack_bf16x2(acc[i][j][4 * r + 2], acc[i][j][4 * r + 3])};
+                    const uint32_t off =
+                        (row < rows && n < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)n) * 2u : kOOR;
+                    __builtin_amdgcn_raw_buffer_store_b64(val, cres, off, 0, 0);
+                }
+        }
+    }
+}
+
+// Compute units of the current device (the persistent grid's size), looked
+// up once per device.
+int num_cus()
+{
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    int* slot = dev < 64 ? &cache[dev] : nullptr;
+    if (slot && *slot > 0) return *slot;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (slot) *slot = n;
+    return n;
+}
+
+}  // namespace
+}  // namespace et
+
+using namespace et;
+
+extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
+                              const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
+                              int64_t slot_capacity, void* c, void* stream)
+{
+    const char* fn = "et_expert_gemm";
+    const int64_t E = num_experts;
+    if (E < 1 || E > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_EXPERTS) + "]");
+    if (K < 8 || K % 8 != 0 || K >= (int64_t(1) << 22))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": K must be a positive multiple of 8 below 2^22");
+    if (N < 8 || N % 8 != 0)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N must be a positive multiple of 8");
+    if (N * K * 2 >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": one expert's weight (N * K * 2 bytes) must be below 2 GiB");
+    if (kBM * N * 2 >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N too large");
+    if (slot_capacity < 0 || slot_capacity >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": slot_capacity out of range");
+    const bool gather = sorted_token != nullptr;
+    if (gather && (a_rows < 0 || a_rows * K * 2 >= (int64_t(1) << 31)))
+        return fail(ET_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": in gather mode the token rows (a_rows * K * 2 bytes) must be below 2 GiB");
+    if (slot_capacity == 0) return ET_OK;
+    if (!a || !w || !expert_offsets || !c) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null pointer");
+    if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15) ||
+        (reinterpret_cast<uintptr_t>(c) & 7))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": a and w must be 16-byte aligned, c 8-byte aligned");
+    const int64_t nN = (N + kBN - 1) / kBN;
+    const int64_t qmax = ((slot_capacity + kBM - 1) / kBM + E) * nN;
+    if (qmax >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": too many output tiles (slot_capacity / 256 * N / 256)");
+    const int64_t blocks = std::min<int64_t>((int64_t)num_cus(), qmax);
+    const dim3 grid((unsigned)(8 * ((blocks + 7) / 8)));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const GemmArgs args{static_cast<const uint16_t*>(a), sorted_token, static_cast<const uint16_t*>(w),
+                        expert_offsets, static_cast<uint16_t*>(c), a_rows, slot_capacity, (int)K, (int)N, (int)E};
+    if (gather) expert_gemm_kernel<true><<<grid, dim3(kThreads), 0, s>>>(args);
+    else expert_gemm_kernel<false><<<grid, dim3(kThreads), 0, s>>>(args);
+    return check_launch("expert_gemm_kernel");
+}

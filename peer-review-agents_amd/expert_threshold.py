@@ -348,6 +348,54 @@ def router_weight_grad(dlogits: torch.Tensor, x: torch.Tensor, out: Optional[tor
 
 
 # --------------------------------------------------------------------------- #
+# expert grouped GEMM
+# --------------------------------------------------------------------------- #
+
+def expert_gemm(a: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: bool = True,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Grouped expert GEMM over the plan's slot blocks (bf16, binary32 accumulation).
+
+    out[s] = A[row(s)] @ W[e(s)]^T for every routed slot s, e(s) its expert.
+    gather=True: ``a`` is the token matrix X [T, K] and row(s) = the slot's token
+    (the dispatch fused into the GEMM: Xp is never materialised).
+    gather=False: ``a`` is slot-major [rows, K] (e.g. dispatch(X) or an
+    activation of the previous projection) and row(s) = s.
+    ``w`` is [E, N, K], each expert's weight in nn.Linear layout.  Returns
+    [rows, N] bf16; rows of ``out`` past the routed slots are left as they were.
+    """
+    _require(a, "a", torch.bfloat16, 2)
+    dev = a.device
+    _require(w, "w", torch.bfloat16, 3, dev)
+    _check_plan(plan, dev)
+    E, N, K = w.shape
+    if E != plan.num_experts:
+        raise ValueError(f"w has {E} experts, plan has {plan.num_experts}")
+    if a.shape[1] != K:
+        raise ValueError(f"a has row length {a.shape[1]}, w has K = {K}")
+    if K < 8 or K % 8 or K >= 1 << 22:
+        raise ValueError(f"K must be a positive multiple of 8 below 2^22, got {K}")
+    if N < 8 or N % 8:
+        raise ValueError(f"N must be a positive multiple of 8, got {N}")
+    if N * K * 2 >= 1 << 31:
+        raise ValueError("one expert's weight must be below 2 GiB")
+    if gather:
+        if a.shape[0] != plan.num_tokens:
+            raise ValueError(f"a has {a.shape[0]} rows, plan has {plan.num_tokens} tokens")
+        if a.shape[0] * K * 2 >= 1 << 31:
+            raise ValueError("in gather mode the token matrix must be below 2 GiB")
+    elif a.shape[0] != plan.rows:
+        raise ValueError(f"a has {a.shape[0]} rows, plan has {plan.rows} slots")
+    c = _out_or_new(out, (plan.rows, N), torch.bfloat16, dev, "out")
+    if a.data_ptr() % 16 or w.data_ptr() % 16 or c.data_ptr() % 8:
+        raise ValueError("a and w must be 16-byte aligned, out 8-byte aligned")
+    with torch.cuda.device(dev):
+        rc = lib().et_expert_gemm(_vp(a), a.shape[0], _vp(plan.sorted_token) if gather else None, _vp(w),
+                                  _vp(plan.expert_offsets), E, K, N, plan.rows, _vp(c), _stream(dev))
+    check("et_expert_gemm", rc)
+    return c
+
+
+# --------------------------------------------------------------------------- #
 # EMA threshold update
 # --------------------------------------------------------------------------- #
 
