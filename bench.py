@@ -10,7 +10,10 @@ resident in HBM before timing starts:
 The router producer (router logits GEMM, fused producer + routing) and its
 backward (dispatch backward with the router input gradient, router weight
 gradient) are measured separately after the timed steps and reported in
-"router_producer" and "router_backward".
+"router_producer" and "router_backward"; so is the expert grouped GEMM that
+consumes the dispatch ("expert_gemm": the gate/up projection with the dispatch
+fused into its operand load, the down projection, and torch's grouped GEMM on
+the same shapes).
 Yp and dXp are separate resident buffers standing in for the expert FFN's
 output and input-gradient (the FFN itself is not part of the path).
 
@@ -219,6 +222,62 @@ def router_backward(et, dev, stream, plan, X, DXP, DGATE, DL, reps: int = 10) ->
     return out
 
 
+EXPERT_FFN = 1536          # expert FFN width of the gate/up and down projections (Qwen3-MoE's, d = 4096, E = 128)
+MFMA_BF16_PEAK = 2.5e15   # MI355X dense bf16 matrix peak, FLOP/s
+
+
+def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
+    """The expert grouped GEMM on the workload's routing: the gate/up projection
+    (K = d, N = 2 * EXPERT_FFN) straight from X with the dispatch fused into the
+    operand load, and the down projection (K = EXPERT_FFN, N = d) on a
+    slot-major operand, each against torch's grouped GEMM (hipBLASLt) -- which
+    needs the dispatched Xp, so the dispatch is timed beside it.  Random-init
+    expert weights of that shape; measured after the timed step with HIP events
+    on the stream the kernels run on."""
+    import torch
+    T, d = X.shape
+    E, S, F = plan.num_experts, plan.rows, EXPERT_FFN
+    g = torch.Generator(device=dev)
+    g.manual_seed(4244)
+    w1 = (torch.randn(E, 2 * F, d, device=dev, generator=g) * d ** -0.5).to(torch.bfloat16)
+    w2 = (torch.randn(E, d, F, device=dev, generator=g) * F ** -0.5).to(torch.bfloat16)
+    h = torch.empty(S, 2 * F, dtype=torch.bfloat16, device=dev)
+    a2 = torch.randn(S, F, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(S, d, dtype=torch.bfloat16, device=dev)
+    xp = et.dispatch(X, plan)
+    offs = plan.expert_offsets[1:].contiguous()
+
+    def timed(fn):
+        fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    t_up = timed(lambda: et.expert_gemm(X, w1, plan, out=h))
+    t_down = timed(lambda: et.expert_gemm(a2, w2, plan, gather=False, out=y))
+    t_disp = timed(lambda: et.dispatch(X, plan, out=xp))
+    w1t, w2t = w1.transpose(1, 2), w2.transpose(1, 2)
+    t_up_lib = timed(lambda: torch._grouped_mm(xp, w1t, offs=offs))
+    t_down_lib = timed(lambda: torch._grouped_mm(a2, w2t, offs=offs))
+    fl_up, fl_down = 2.0 * S * d * 2 * F, 2.0 * S * F * d
+    del w1, w2, h, a2, y, xp
+    return {"kernel": "expert_gemm_kernel", "expert_ffn": F,
+            "gate_up": {"K": d, "N": 2 * F, "mode": "gather (dispatch fused)", "ms": round(t_up, 3),
+                        "TFLOP/s": round(fl_up / (t_up * 1e-3) / 1e12, 1),
+                        "frac": round(fl_up / (t_up * 1e-3) / MFMA_BF16_PEAK, 4),
+                        "torch_grouped_mm_ms": round(t_up_lib, 3), "dispatch_ms": round(t_disp, 3),
+                        "torch_dispatch_plus_grouped_mm_ms": round(t_disp + t_up_lib, 3)},
+            "down": {"K": F, "N": d, "mode": "slot-major", "ms": round(t_down, 3),
+                     "TFLOP/s": round(fl_down / (t_down * 1e-3) / 1e12, 1),
+                     "frac": round(fl_down / (t_down * 1e-3) / MFMA_BF16_PEAK, 4),
+                     "torch_grouped_mm_ms": round(t_down_lib, 3)}}
+
+
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
     """The CPU restatement (oracle/, single thread) on the first `tokens`
     tokens of the same workload, running the same five operations as one GPU
@@ -393,6 +452,14 @@ def main() -> int:
           f"({100 * rb['router_wgrad_frac']:.1f}% of peak; torch f32 mm {rb['torch_mm_f32_wgrad_us']:.1f} us)"
           if "router_wgrad_us" in rb else ""), file=sys.stderr)
 
+    eg = None
+    if act == torch.bfloat16 and d % 8 == 0 and S > 0:
+        eg = expert_gemm_leg(et, dev, stream, plan_obj, X)
+        gu, dn = eg["gate_up"], eg["down"]
+        print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; torch grouped "
+              f"{gu['torch_grouped_mm_ms']:.3f} ms + dispatch {gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms "
+              f"({dn['TFLOP/s']:.0f} TFLOP/s; torch grouped {dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
+
     cpu = None
     if args.cpu_tokens > 0:
         cpu = cpu_baseline(args.workload, args.seed, min(args.cpu_tokens, T))
@@ -422,6 +489,7 @@ def main() -> int:
         "threshold_dynamics": dyn,
         "router_producer": rp,
         "router_backward": rb,
+        "expert_gemm": eg,
         "kernels": kernels,
     }
     for name in STAGES:

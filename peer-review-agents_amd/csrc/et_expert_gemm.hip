@@ -96,6 +96,15 @@ __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t res, uint32_t vo
                  : "memory");
 }
 
+// L2 prefetch: a 4-byte direct-to-LDS load per lane, all of a wave's into one
+// scratch area of LDS that nothing reads (a load into a register that is never
+// read could land after the register has been given to another value).
+__device__ __forceinline__ void prefetch_line(__amdgpu_buffer_rsrc_t res, uint32_t voff, uint32_t soff, uint32_t lds)
+{
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(res), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight,
 // then meet the other waves.  The direct-to-LDS loads count in vmcnt and are
 // in LDS once it has dropped, so after the barrier every wave's loads of the
@@ -114,6 +123,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
 {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kStage];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
+    __shared__ __attribute__((aligned(256))) uint32_t pf_sink[64];   // target of the L2 prefetches
 
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -203,6 +213,24 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             const int n = n0 + R;
             boff[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
         }
+        // L2 prefetch rows: wave w touches the line of A row and W row 64 w + lane.
+        uint32_t pfa, pfb;
+        {
+            const int R = 64 * wave + lane;
+            const int row = min(R, rows - 1);
+            if constexpr (GATHER) {
+                const int tok = g.sorted_token[s0 + row];
+                pfa = (uint32_t)tok < (uint32_t)g.a_rows ? (uint32_t)tok * (uint32_t)K * 2u : kOOR;
+            } else {
+                pfa = (uint32_t)row * (uint32_t)K * 2u;
+            }
+            pfb = n0 + R < N ? (uint32_t)(n0 + R) * (uint32_t)K * 2u : kOOR;
+        }
+        const uint32_t sink = (uint32_t)(uintptr_t)(lds_t*)pf_sink;
+        auto prefetch = [&](int c) {
+            prefetch_line(ares, pfa, (uint32_t)c * 128u, sink);
+            prefetch_line(wres, pfb, (uint32_t)c * 128u, sink);
+        };
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
         // chunk c -> stage c & 1; the chunk's column offset c * 128 bytes
         // goes in the scalar offset.  A chunk that runs past K masks the
@@ -265,6 +293,8 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+        if (nk > 2) prefetch(2);
+        if (nk > 3) prefetch(3);
         issue(0);
         dma_wait_barrier<0>();
         if (nk > 1) issue(1);
@@ -275,7 +305,11 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         // for its fragment reads and for chunk c + 1, then meets the others:
         // from there chunk c + 1 is visible, nobody reads chunk c any more,
         // so chunk c + 2 may refill its stage, and chunk c + 1's first
-        // fragments load under the last k-step's MFMAs.
+        // fragments load under the last k-step's MFMAs.  LDS holds only two
+        // stages, so each chunk is also touched two steps ahead: one 4-byte
+        // read per operand row, which brings the first 64-byte sector of
+        // the row's line into L2 (at C3 this is ~4% faster; touching both
+        // sectors costs the load path more instructions than it saves).
         for (int c = 0; c < nk; ++c) {
             read_frags(c, 1, f[1]);
             __builtin_amdgcn_sched_barrier(0);
@@ -291,8 +325,12 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             __builtin_amdgcn_sched_barrier(0);
             if (c + 1 < nk) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                dma_wait_barrier<0>();
+                // Issued after chunk c + 1 (in step c - 1): the 2 prefetches
+                // of chunk c + 3, if it exists.  vmcnt retires in issue order.
+                if (c >= 1 && c + 3 < nk) dma_wait_barrier<2>();
+                else dma_wait_barrier<0>();
                 if (c + 2 < nk) issue(c + 2);
+                if (c + 4 < nk) prefetch(c + 4);
                 read_frags(c + 1, 0, f[0]);
             }
             __builtin_amdgcn_sched_barrier(0);
