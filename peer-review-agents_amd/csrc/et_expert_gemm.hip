@@ -13,16 +13,19 @@
 // Tiling.  A block of 4 waves owns 256 slots x 256 output features of one
 // expert; wave (wm, wn) owns 128 x 128 of it, 4 x 4 tiles of
 // v_mfma_f32_32x32x16_bf16.  K advances in chunks of 64 through two LDS stages
-// filled by gfx950's direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds):
-// no staging registers, and chunk c + 1 streams in while chunk c is
-// multiplied.  One direct load fills 1 KiB of LDS, lane i's 16 bytes at 16 i;
-// it is given 8 operand rows x 128 contiguous bytes (a whole cache line per
-// row: streaming through L2 into LDS runs ~45% faster this way than with 32
-// rows x 32 bytes per instruction, the MFMA fragment's own shape).  So a stage
-// holds each operand row-major, 128 bytes (64 k) per row, and the 16-byte
-// segment s of row R sits at slot s ^ key(R), key(R) = (R & 7) ^ ((R >> 3) & 1):
-// the fragment reads (lane l: row l % 32, segment 2 * kstep + l / 32) then hit
-// 16 distinct slots of every 256-byte bank window, with no bank conflicts.
+// filled by gfx950's direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds),
+// with no staging registers.  A wave holds a whole chunk's MFMA fragments in
+// registers, so a stage is free again as soon as every wave has read it, and
+// two chunks stream in while one is multiplied.  One direct load fills 1 KiB
+// of LDS, lane i's 16 bytes at 16 i; it is given 8 operand rows x 128
+// contiguous bytes (a whole cache line per row: streaming through L2 into LDS
+// runs ~45% faster this way than with 32 rows x 32 bytes per instruction, the
+// MFMA fragment's own shape).  So a stage holds each operand row-major, 128
+// bytes (64 k) per row, and the 16-byte segment s of row R sits at slot
+// s ^ key(R), key(R) = (R & 7) ^ ((R >> 3) & 1): the fragment reads (lane l:
+// row l % 32, segment 2 * kstep + l / 32) then hit 16 distinct slots of every
+// 256-byte bank window, with no bank conflicts.  The output tile goes back
+// through LDS so that it is stored in whole rows.
 //
 // MFMA 32x32x16 bf16 operand layout (checked on the device by the router
 // kernels): lane l holds A row l % 32 and B column l % 32 at k = 8 (l / 32) + i;
@@ -60,6 +63,8 @@ constexpr int kBufDword3 = 0x00020000;
 // A byte offset past every descriptor's num_records (all < 2^31): loads return
 // 0 and stores are dropped.
 constexpr uint32_t kOOR = 0x80000000u;
+// s_waitcnt immediate of gfx9 for lgkmcnt(0) alone (vmcnt 63, expcnt 7: no wait)
+constexpr int kWaitLgkm0 = 0xC07F;
 
 constexpr int kBM = 256;          // slots per tile
 constexpr int kBN = 256;          // output features per tile
@@ -68,6 +73,8 @@ constexpr int kThreads = 256;
 constexpr int kGroupM = 8;        // slot tiles per group in the tile order
 constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
 constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
+constexpr int kOutPitch = 2 * kBN + 16;   // bytes per row of the output tile staged in LDS
+constexpr int kSmemBytes = 2 * kStage > kBM * kOutPitch ? 2 * kStage : kBM * kOutPitch;
 
 struct GemmArgs {
     const uint16_t* a;              // gather: X [a_rows, K]; else A [cap, K]
@@ -96,15 +103,6 @@ __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t res, uint32_t vo
                  : "memory");
 }
 
-// L2 prefetch: a 4-byte direct-to-LDS load per lane, all of a wave's into one
-// scratch area of LDS that nothing reads (a load into a register that is never
-// read could land after the register has been given to another value).
-__device__ __forceinline__ void prefetch_line(__amdgpu_buffer_rsrc_t res, uint32_t voff, uint32_t soff, uint32_t lds)
-{
-    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(res), "s"(soff), "{m0}"(lds)
-                 : "memory");
-}
-
 // Wait until at most N of this wave's vector-memory operations are in flight,
 // then meet the other waves.  The direct-to-LDS loads count in vmcnt and are
 // in LDS once it has dropped, so after the barrier every wave's loads of the
@@ -121,9 +119,9 @@ __device__ __forceinline__ void dma_wait_barrier()
 template <bool GATHER>
 __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
 {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kStage];
+    // the two operand stages, and at the end of a tile the bf16 output tile
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
-    __shared__ __attribute__((aligned(256))) uint32_t pf_sink[64];   // target of the L2 prefetches
 
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -213,46 +211,25 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             const int n = n0 + R;
             boff[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
         }
-        // L2 prefetch rows: wave w touches the line of A row and W row 64 w + lane.
-        uint32_t pfa, pfb;
-        {
-            const int R = 64 * wave + lane;
-            const int row = min(R, rows - 1);
-            if constexpr (GATHER) {
-                const int tok = g.sorted_token[s0 + row];
-                pfa = (uint32_t)tok < (uint32_t)g.a_rows ? (uint32_t)tok * (uint32_t)K * 2u : kOOR;
-            } else {
-                pfa = (uint32_t)row * (uint32_t)K * 2u;
-            }
-            pfb = n0 + R < N ? (uint32_t)(n0 + R) * (uint32_t)K * 2u : kOOR;
-        }
-        const uint32_t sink = (uint32_t)(uintptr_t)(lds_t*)pf_sink;
-        auto prefetch = [&](int c) {
-            prefetch_line(ares, pfa, (uint32_t)c * 128u, sink);
-            prefetch_line(wres, pfb, (uint32_t)c * 128u, sink);
-        };
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
         // chunk c -> stage c & 1; the chunk's column offset c * 128 bytes
         // goes in the scalar offset.  A chunk that runs past K masks the
         // segments at or past K (K is a multiple of 8, so a segment is all
         // in or all out).
-        auto issue = [&](int c) {
-            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u;
+        // One direct load of chunk c: q even -> A block q / 2, q odd -> W block
+        // q / 2.  A chunk that runs past K masks the segments at or past K
+        // (K is a multiple of 8, so a segment is all in or all out).
+        auto dma_one = [&](int c, int q) {
+            const int i = q >> 1;
+            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u + (uint32_t)i * 1024u;
             const uint32_t soff = (uint32_t)c * 128u;
-            if ((c + 1) * kKC <= K) {
+            const uint32_t kmask = (c + 1) * kKC <= K || c * kKC + segk[i & 1] < K ? 0u : kOOR;
+            if (q & 1) dma_b128(wres, boff[i] | kmask, soff, sb + kHalf);
+            else dma_b128(ares, aoff[i] | kmask, soff, sb);
+        };
+        auto issue = [&](int c) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    dma_b128(ares, aoff[i], soff, sb + i * 1024);
-                    dma_b128(wres, boff[i], soff, sb + kHalf + i * 1024);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t kmask = c * kKC + segk[i & 1] < K ? 0u : kOOR;
-                    dma_b128(ares, aoff[i] | kmask, soff, sb + i * 1024);
-                    dma_b128(wres, boff[i] | kmask, soff, sb + kHalf + i * 1024);
-                }
-            }
+            for (int q = 0; q < 16; ++q) dma_one(c, q);
         };
 
         f32x16_t acc[4][4];
@@ -268,99 +245,134 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int flane = ((lane & 31) >> 3) * 1024 + (lane & 7) * 128;
         const unsigned char* const abase = smem + wm * 16384 + flane;
         const unsigned char* const bbase = smem + kHalf + wn * 16384 + flane;
-        u32x4_t f[2][2][4];       // [buffer][A, W][tile]
-        auto read_frags = [&](int c, int ks, u32x4_t (&fr)[2][4]) {
-            const int off = (c & 1) * kStage + (((2 * ks + (lane >> 5)) ^ fkey) << 4);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) fr[0][t] = *reinterpret_cast<const u32x4_t*>(abase + off + t * 4096);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) fr[1][t] = *reinterpret_cast<const u32x4_t*>(bbase + off + t * 4096);
+        u32x4_t f[4][2][4];       // [k-step][A, W][tile]: a whole chunk's fragments
+        // fragment q of k-step ks (q < 4: A tile q, else W tile q - 4)
+        auto frag_one = [&](int c, int ks, int q) {
+            const int off = (c & 1) * kStage + (((2 * ks + (lane >> 5)) ^ fkey) << 4) + (q & 3) * 4096;
+            f[ks][q >> 2][q & 3] = *reinterpret_cast<const u32x4_t*>((q < 4 ? abase : bbase) + off);
         };
-        auto mfmas = [&](const u32x4_t (&fr)[2][4]) {
+        auto read_frags = [&](int c, int ks) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fr[1][j]),
-                                                                        __builtin_bit_cast(bf16x8_t, fr[0][i]),
-                                                                        acc[i][j], 0, 0, 0);
+            for (int q = 0; q < 8; ++q) frag_one(c, ks, q);
+        };
+        // MFMA m of k-step ks: slot tile m / 4, feature tile m % 4
+        auto mfma_one = [&](int ks, int m) {
+            const int i = m >> 2, j = m & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
+                                                                __builtin_bit_cast(bf16x8_t, f[ks][0][i]), acc[i][j],
+                                                                0, 0, 0);
+        };
+        auto pin = [&]() { __builtin_amdgcn_sched_barrier(0); };
+        auto barrier = [&]() {
+            pin();
+            asm volatile("s_barrier" ::: "memory");
+            pin();
         };
 
         // Every wave has finished reading the previous tile's stages (its
-        // last fragment reads were consumed by its MFMAs).  Only the previous
-        // tile's stores can be in flight; the first wait below counts them
-        // with the loads, since vmcnt retires in issue order.
+        // last fragment reads were consumed by its MFMAs), and the epilogue's
+        // LDS reads were consumed by its stores.  Only the previous tile's
+        // stores can be in flight; the first wait below counts them with the
+        // loads, since vmcnt retires in issue order.
+        barrier();
+        issue(0);
+        if (nk > 1) issue(1);
+        if (nk > 1) dma_wait_barrier<16>();
+        else dma_wait_barrier<0>();
+        read_frags(0, 0);
+        read_frags(0, 1);
+        read_frags(0, 2);
+        // Step c (chunk c in stage c & 1, its k-steps 0..2 already in
+        // registers).  Each wave reads the chunk's last k-step, so once it
+        // has waited for its reads and met the others, nobody reads stage
+        // c & 1 any more: chunk c + 2 is loaded into it while k-steps 1 and 2
+        // multiply.  Then every wave waits for chunk c + 1 (chunk c + 2's 16
+        // loads per wave may stay in flight), meets the others, and reads
+        // chunk c + 1's k-steps 0..2 under k-step 3's MFMAs.  So two chunks
+        // stream in while one is multiplied, with two LDS stages.  A wave
+        // issues in order, so every load and fragment read sits between two
+        // MFMAs (the order is pinned): the matrix pipe keeps a queued MFMA
+        // while they issue.
+        for (int c = 0; c < nk; ++c) {
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                mfma_one(0, m);
+                pin();
+                if (m < 8) frag_one(c, 3, m);
+                pin();
+            }
+            // (the builtin, not inline assembly: the compiler then knows these
+            // reads are complete and adds no waits for them later)
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            barrier();
+            const bool more2 = c + 2 < nk;
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                mfma_one(1 + (m >> 4), m & 15);
+                pin();
+                if (more2 && (m & 1)) dma_one(c + 2, m >> 1);
+                pin();
+            }
+            const bool more1 = c + 1 < nk;
+            if (more1) {
+                if (more2) dma_wait_barrier<16>();
+                else dma_wait_barrier<0>();
+            }
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                mfma_one(3, m);
+                pin();
+                if (more1) {
+                    const int r0 = (3 * m) / 2, r1 = (3 * m + 3) / 2;   // 24 reads over 16 MFMAs
+                    for (int r = r0; r < r1; ++r) frag_one(c + 1, r >> 3, r & 7);
+                }
+                pin();
+            }
+        }
+
+        // Epilogue, through LDS so that the stores are whole rows: every wave
+        // has issued its last MFMAs (their fragment reads are done), so after
+        // a barrier the stages are free.  Lane l holds slot (wm * 4 + i) * 32 +
+        // l % 32 and features (wn * 4 + j) * 32 + 8 r + 4 (l / 32) + 0..3 in
+        // acc[i][j][4 r ..]; they go to the bf16 tile [256 rows][kOutPitch
+        // bytes] (the 16 bytes of padding put the 32 rows of one write on
+        // distinct banks).  Then each wave stores 64 rows, two 512-byte rows
+        // per instruction, with range-checked stores: rows past the tile's
+        // slots and features past N get an out-of-range offset and are
+        // dropped.
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        if (nk > 2) prefetch(2);
-        if (nk > 3) prefetch(3);
-        issue(0);
-        dma_wait_barrier<0>();
-        if (nk > 1) issue(1);
-        read_frags(0, 0, f[0]);
-        // Step c (chunk c in stage c & 1, chunk c + 1 streaming into the
-        // other): k-steps 0..2 read the next k-step's fragments while their
-        // own MFMAs issue.  Before the last k-step's MFMAs every wave waits
-        // for its fragment reads and for chunk c + 1, then meets the others:
-        // from there chunk c + 1 is visible, nobody reads chunk c any more,
-        // so chunk c + 2 may refill its stage, and chunk c + 1's first
-        // fragments load under the last k-step's MFMAs.  LDS holds only two
-        // stages, so each chunk is also touched two steps ahead: one 4-byte
-        // read per operand row, which brings the first 64-byte sector of
-        // the row's line into L2 (at C3 this is ~4% faster; touching both
-        // sectors costs the load path more instructions than it saves).
-        for (int c = 0; c < nk; ++c) {
-            read_frags(c, 1, f[1]);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(f[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            read_frags(c, 2, f[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(f[1]);
-            __builtin_amdgcn_sched_barrier(0);
-            read_frags(c, 3, f[1]);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(f[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            if (c + 1 < nk) {
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                // Issued after chunk c + 1 (in step c - 1): the 2 prefetches
-                // of chunk c + 3, if it exists.  vmcnt retires in issue order.
-                if (c >= 1 && c + 3 < nk) dma_wait_barrier<2>();
-                else dma_wait_barrier<0>();
-                if (c + 2 < nk) issue(c + 2);
-                if (c + 4 < nk) prefetch(c + 4);
-                read_frags(c + 1, 0, f[0]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(f[1]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-
-        // Epilogue: lane l holds slot (wm * 4 + i) * 32 + l % 32 and features
-        // (wn * 4 + j) * 32 + 8 (r / 4) + 4 (l / 32) + 0..3 in acc[i][j][4 (r / 4) ..].
-        // Range-checked stores: rows past the tile's slots and features past N
-        // are given an out-of-range offset and dropped.
-        const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * N, (short)0, rows * N * 2,
-                                                                               kBufDword3);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = (wm * 4 + i) * 32 + r32;
+            unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitch;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int n = n0 + (wn * 4 + j) * 32 + 8 * r + 4 * kh;
+                    const int col = (wn * 4 + j) * 32 + 8 * r + 4 * kh;
                     const u32x2_t val = {pack_bf16x2(acc[i][j][4 * r], acc[i][j][4 * r + 1]),
                                          pack_bf16x2(acc[i][j][4 * r + 2], acc[i][j][4 * r + 3])};
-                    const uint32_t off =
-                        (row < rows && n < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)n) * 2u : kOOR;
-                    __builtin_amdgcn_raw_buffer_store_b64(val, cres, off, 0, 0);
+                    *reinterpret_cast<u32x2_t*>(orow + col * 2) = val;
                 }
+        }
+        __syncthreads();
+        const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * N, (short)0, rows * N * 2,
+                                                                               kBufDword3);
+        {
+            const int n = n0 + (lane & 31) * 8;
+#pragma unroll 4
+            for (int q = 0; q < 32; ++q) {
+                const int row = wave * 64 + 2 * q + kh;
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * kOutPitch + (lane & 31) * 16);
+                const uint32_t off =
+                    (row < rows && n < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)n) * 2u : kOOR;
+                __builtin_amdgcn_raw_buffer_store_b128(v, cres, off, 0, 0);
+            }
         }
     }
 }
+
 
 // Compute units of the current device (the persistent grid's size), looked
 // up once per device.
