@@ -231,7 +231,8 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     (K = d, N = 2 * EXPERT_FFN) straight from X with the dispatch fused into the
     operand load, and the down projection (K = EXPERT_FFN, N = d) on a
     slot-major operand, each against torch's grouped GEMM (hipBLASLt) -- which
-    needs the dispatched Xp, so the dispatch is timed beside it.  Random-init
+    needs the dispatched Xp, so the dispatch is timed beside it.  The gate/up
+    projection is also timed with the SwiGLU epilogue (half the output).  Random-init
     expert weights of that shape; measured after the timed step with HIP events
     on the stream the kernels run on."""
     import torch
@@ -259,6 +260,9 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
         return a.elapsed_time(b) / reps
 
     t_up = timed(lambda: et.expert_gemm(X, w1, plan, out=h))
+    hs = torch.empty(S, F, dtype=torch.bfloat16, device=dev)
+    t_up_swiglu = timed(lambda: et.expert_gemm(X, w1, plan, epilogue="swiglu", out=hs))
+    del hs
     t_down = timed(lambda: et.expert_gemm(a2, w2, plan, gather=False, out=y))
     t_disp = timed(lambda: et.dispatch(X, plan, out=xp))
     w1t, w2t = w1.transpose(1, 2), w2.transpose(1, 2)
@@ -271,7 +275,8 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
                         "TFLOP/s": round(fl_up / (t_up * 1e-3) / 1e12, 1),
                         "frac": round(fl_up / (t_up * 1e-3) / MFMA_BF16_PEAK, 4),
                         "torch_grouped_mm_ms": round(t_up_lib, 3), "dispatch_ms": round(t_disp, 3),
-                        "torch_dispatch_plus_grouped_mm_ms": round(t_disp + t_up_lib, 3)},
+                        "torch_dispatch_plus_grouped_mm_ms": round(t_disp + t_up_lib, 3),
+                        "swiglu_epilogue_ms": round(t_up_swiglu, 3)},
             "down": {"K": F, "N": d, "mode": "slot-major", "ms": round(t_down, 3),
                      "TFLOP/s": round(fl_down / (t_down * 1e-3) / 1e12, 1),
                      "frac": round(fl_down / (t_down * 1e-3) / MFMA_BF16_PEAK, 4),
@@ -456,9 +461,10 @@ def main() -> int:
     if act == torch.bfloat16 and d % 8 == 0 and S > 0:
         eg = expert_gemm_leg(et, dev, stream, plan_obj, X)
         gu, dn = eg["gate_up"], eg["down"]
-        print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; torch grouped "
-              f"{gu['torch_grouped_mm_ms']:.3f} ms + dispatch {gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms "
-              f"({dn['TFLOP/s']:.0f} TFLOP/s; torch grouped {dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
+        print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; with the SwiGLU "
+              f"epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} ms + dispatch "
+              f"{gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; torch grouped "
+              f"{dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
 
     cpu = None
     if args.cpu_tokens > 0:

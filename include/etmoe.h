@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 4
+#define ET_ABI_VERSION 5
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -245,32 +245,43 @@ int et_router_route(const void* x, const void* w, const float* thr, int64_t num_
                     int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
                     float* logits, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Epilogues of et_expert_gemm. */
+#define ET_GEMM_PLAIN 0      /* c = the product                                      */
+#define ET_GEMM_ROW_SCALE 1  /* c[s, :] = row_scale[s] * the product (binary32)      */
+#define ET_GEMM_SWIGLU 2     /* c[s, f] = (g * sigmoid(g)) * u, g = product column f,
+                                u = product column F + f, F = N / 2 (binary32)       */
+
 /*
  * Expert grouped GEMM over the routing CSR (the expert FFN's projections):
- *   c[s, n] = sum_k a[row(s), k] * w[e(s), n, k]   (bf16 operands, binary32
- *                                                   accumulation, bf16 out)
+ *   p[s, n] = sum_k a[row(s), k] * w[e(s), n, k]   (bf16 operands, binary32
+ *                                                   accumulation)
  * for every slot s below min(expert_offsets[E], slot_capacity), e(s) the
- * expert whose block [expert_offsets[e], expert_offsets[e + 1]) holds s.
+ * expert whose block [expert_offsets[e], expert_offsets[e + 1]) holds s, and
+ * c[s, :] = the epilogue of p[s, :], rounded once to bf16.
  *   sorted_token != NULL (gather mode): row(s) = sorted_token[s] and a is the
  *       token matrix X bf16 [a_rows = T, K] -- the dispatch fused into the
  *       operand load, so Xp is never written;
  *   sorted_token == NULL: row(s) = s and a is slot-major bf16
  *       [slot_capacity, K] (a_rows is ignored).
  *   w bf16 [E, N, K]: expert e's weight in nn.Linear layout (row n = output
- *       feature n); c bf16 [slot_capacity, N].
- * K a multiple of 8 below 2^22, N a multiple of 8, N*K*2 below 2^31 bytes;
- * in gather mode a_rows*K*2 below 2^31 bytes.  a and w 16-byte aligned, c
- * 8-byte aligned.  Rows of c past the routed slots are left as they were.
- * Every output sums its k-steps of 16 in ascending k (each k-step inside one
- * MFMA), so the gather and slot-major modes give identical bits, repeated
- * calls give identical bits, and integer-valued inputs whose partial sums stay
- * below 2^24 give the exact result rounded once to bf16.
+ *       feature n).  c bf16 [slot_capacity, N], or [slot_capacity, N / 2] for
+ *       ET_GEMM_SWIGLU, whose weight holds the gate rows then the up rows.
+ *   row_scale f32 [slot_capacity] (ET_GEMM_ROW_SCALE only; may be NULL
+ *       otherwise), e.g. slot_gate: a per-slot factor commutes with the sum.
+ *   sigmoid is the one routing uses (one exp of -|g|, one division).
+ * K a multiple of 8 below 2^22, N a multiple of 8 (of 16 for SwiGLU),
+ * N*K*2 below 2^31 bytes; in gather mode a_rows*K*2 below 2^31 bytes.  a, w
+ * and c 16-byte aligned.  Rows of c past the routed slots are left as they
+ * were.  Every output sums its k-steps of 16 in ascending k (each k-step
+ * inside one MFMA), so the gather and slot-major modes give identical bits,
+ * repeated calls give identical bits, and integer-valued inputs whose partial
+ * sums stay below 2^24 give the exact product before the epilogue.
  * Implements the expert grouped GEMM that consumes the dispatch (no reference
  * counterpart).
  */
 int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
                    const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
-                   int64_t slot_capacity, void* c, void* stream);
+                   int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_exp_nonpos.argtypes = [ctypes.c_float]
         L.oracle_sigmoid.restype = ctypes.c_float
         L.oracle_sigmoid.argtypes = [ctypes.c_float]
+        L.oracle_swiglu.restype = ctypes.c_float
+        L.oracle_swiglu.argtypes = [ctypes.c_float, ctypes.c_float]
         L.oracle_sigmoid_order_scan.restype = None
         L.oracle_sigmoid_order_scan.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _p]
         L.oracle_select.restype = _i64
@@ -130,6 +132,17 @@ def sigmoid(logits: np.ndarray) -> np.ndarray:
     for i, v in enumerate(flat):
         out[i] = L.oracle_sigmoid(float(v))
     return out.reshape(np.shape(logits))
+
+
+def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """Element-wise (g * sigmoid(g)) * u in binary32 (oracle_swiglu; tests only)."""
+    L = lib()
+    gf = _c(g, np.float32).ravel()
+    uf = _c(u, np.float32).ravel()
+    out = np.empty_like(gf)
+    for i in range(gf.size):
+        out[i] = L.oracle_swiglu(float(gf[i]), float(uf[i]))
+    return out.reshape(np.shape(g))
 
 
 def exp_nonpos(x: np.ndarray) -> np.ndarray:

@@ -111,6 +111,18 @@ float oracle_sigmoid(float l)
     return z / (1.0f + z);
 }
 
+/* SwiGLU activation of the expert GEMM's epilogue: h = (g * sigmoid(g)) * u in
+ * binary32, two separately rounded products (no fma), sigmoid as above.  The
+ * specification is this expression; the library's ET_GEMM_SWIGLU epilogue
+ * evaluates it on its binary32 accumulators.  Pinned in tests/test_oracle.py
+ * against float64 silu(g) * u (a few ulps) and exact special values. */
+float oracle_swiglu(float g, float u)
+{
+    const float s = oracle_sigmoid(g);
+    const float gs = g * s;
+    return gs * u;
+}
+
 /* Order scan of the sigmoid: over the floats with order index k in [k0, k1)
  * (k < 2^31: the negative floats from the most negative up to -0, as bit
  * patterns 0xFFFFFFFF - k; k >= 2^31: +0 up to +inf, bit patterns k - 2^31),

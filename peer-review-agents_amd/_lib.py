@@ -22,6 +22,7 @@ ET_DTYPE_F32 = 0
 ET_DTYPE_BF16 = 1
 ET_MAX_EXPERTS = 1024
 ET_MAX_ROUTER_EXPERTS = 256
+ET_GEMM_PLAIN, ET_GEMM_ROW_SCALE, ET_GEMM_SWIGLU = 0, 1, 2
 
 
 class ETMoEError(RuntimeError):
@@ -59,7 +60,7 @@ _SIGNATURES = {
     "et_dispatch_bwd_router": (_int, [_p, _p, _p, _i64, _i64, _int, _i64, _p, _p, _p, _i64, _p, _p, _p, _sz, _p]),
     "et_router_wgrad_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "et_router_wgrad": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _sz, _p]),
-    "et_expert_gemm": (_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "et_expert_gemm": (_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _p, _p]),
 }
 
 _lib = None

@@ -74,6 +74,7 @@ constexpr int kGroupM = 8;        // slot tiles per group in the tile order
 constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
 constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
 constexpr int kOutPitch = 2 * kBN + 16;   // bytes per row of the output tile staged in LDS
+constexpr int kOutPitchHalf = kBN + 16;   // the same for the 128-column SwiGLU tile
 constexpr int kSmemBytes = 2 * kStage > kBM * kOutPitch ? 2 * kStage : kBM * kOutPitch;
 
 struct GemmArgs {
@@ -82,10 +83,18 @@ struct GemmArgs {
     const uint16_t* w;              // [E, N, K]
     const int32_t* expert_offsets;  // [E + 1]
     uint16_t* c;                    // [cap, N]
+    const float* row_scale;         // [cap] (EPI_ROW_SCALE only)
     int64_t a_rows;
     int64_t cap;
-    int K, N, E;
+    int K, N, E;                    // N: rows of each expert's weight (2 F for SwiGLU)
 };
+
+// Epilogues: the plain product; the product times a per-slot factor; or SwiGLU,
+// h = silu(g) * u of the gate rows g (weight rows 0..F-1) and the up rows u
+// (rows F..2F-1) of the same hidden unit.
+constexpr int EPI_PLAIN = ET_GEMM_PLAIN;
+constexpr int EPI_ROW_SCALE = ET_GEMM_ROW_SCALE;
+constexpr int EPI_SWIGLU = ET_GEMM_SWIGLU;
 
 // One direct-to-LDS load: this lane's 16 bytes at byte offset voff + soff of
 // the buffer land at LDS address lds + 16 * lane (soff and lds are
@@ -116,7 +125,7 @@ __device__ __forceinline__ void dma_wait_barrier()
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool GATHER>
+template <bool GATHER, int EPI>
 __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
 {
     // the two operand stages, and at the end of a tile the bf16 output tile
@@ -146,7 +155,10 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     }
     __syncthreads();
 
-    const int nN = (N + kBN - 1) / kBN;
+    // A SwiGLU tile covers 128 hidden units: 128 gate rows and their 128 up
+    // rows of the weight (256 rows, as every tile).
+    const int F = N / 2;
+    const int nN = EPI == EPI_SWIGLU ? (F + kBN / 2 - 1) / (kBN / 2) : (N + kBN - 1) / kBN;
     const int Q = ptile[E] * nN;
     const int per = (Q + 7) / 8;
     const int nloc = (int)(gridDim.x / 8);
@@ -178,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int64_t s0 = (int64_t)g.expert_offsets[e] + (int64_t)mt * kBM;
         const int64_t rend = min<int64_t>(g.expert_offsets[e + 1], g.cap);
         const int rows = (int)min<int64_t>(kBM, rend - s0);
-        const int n0 = nt * kBN;
+        const int n0 = nt * (EPI == EPI_SWIGLU ? kBN / 2 : kBN);   // first output column of the tile
 
         // Direct loads of a chunk: wave w fills row groups 8 w + i (i < 8) of
         // A and of W, rows R = 64 w + 8 i + lane / 8 of the tile; lane puts
@@ -208,8 +220,17 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             } else {
                 aoff[i] = (uint32_t)row * (uint32_t)K * 2u + seg;
             }
-            const int n = n0 + R;
-            boff[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
+            if constexpr (EPI == EPI_SWIGLU) {
+                // tile row R -> wave column half R / 128, MFMA tile (R / 32) % 4
+                // (0, 1: gate; 2, 3: up), so a wave's gate and up accumulators
+                // of one hidden unit sit in the same lane and register
+                const int t = (R >> 5) & 3;
+                const int hid = n0 + (R >> 7) * 64 + (t & 1) * 32 + (R & 31);
+                boff[i] = hid < F ? (uint32_t)(t >= 2 ? F + hid : hid) * (uint32_t)K * 2u + seg : kOOR;
+            } else {
+                const int n = n0 + R;
+                boff[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
+            }
         }
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
         // chunk c -> stage c & 1; the chunk's column offset c * 128 bytes
@@ -333,33 +354,79 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         // Epilogue, through LDS so that the stores are whole rows: every wave
         // has issued its last MFMAs (their fragment reads are done), so after
         // a barrier the stages are free.  Lane l holds slot (wm * 4 + i) * 32 +
-        // l % 32 and features (wn * 4 + j) * 32 + 8 r + 4 (l / 32) + 0..3 in
-        // acc[i][j][4 r ..]; they go to the bf16 tile [256 rows][kOutPitch
-        // bytes] (the 16 bytes of padding put the 32 rows of one write on
-        // distinct banks).  Then each wave stores 64 rows, two 512-byte rows
-        // per instruction, with range-checked stores: rows past the tile's
-        // slots and features past N get an out-of-range offset and are
+        // l % 32 and tile columns (wn * 4 + j) * 32 + 8 r + 4 (l / 32) + 0..3
+        // in acc[i][j][4 r ..].  The bf16 results go to an LDS tile of 256
+        // rows (16 bytes of padding per row put the 32 rows of one write on
+        // distinct banks).  Then each wave stores 64 rows, whole rows per
+        // instruction, with range-checked stores: rows past the tile's slots
+        // and columns past the output get an out-of-range offset and are
         // dropped.
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EPI == EPI_SWIGLU) {
+            // h = (g * sigmoid(g)) * u in binary32, from the gate tiles j = 0, 1
+            // and the up tiles j + 2 of the same lane and register; 128 hidden
+            // columns per tile, wave column half wn holds hidden wn * 64 ...
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitch;
+            for (int i = 0; i < 4; ++i) {
+                unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitchHalf;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int col = (wn * 4 + j) * 32 + 8 * r + 4 * kh;
-                    const u32x2_t val = {pack_bf16x2(acc[i][j][4 * r], acc[i][j][4 * r + 1]),
-                                         pack_bf16x2(acc[i][j][4 * r + 2], acc[i][j][4 * r + 3])};
-                    *reinterpret_cast<u32x2_t*>(orow + col * 2) = val;
+                    for (int r = 0; r < 4; ++r) {
+                        float h[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float gv = acc[i][j][4 * r + e];
+                            h[e] = (gv * sigmoid(gv)) * acc[i][j + 2][4 * r + e];
+                        }
+                        const int col = wn * 64 + j * 32 + 8 * r + 4 * kh;
+                        const u32x2_t val = {pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                        *reinterpret_cast<u32x2_t*>(orow + col * 2) = val;
+                    }
+            }
+            __syncthreads();
+            const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * F, (short)0,
+                                                                                   rows * F * 2, kBufDword3);
+            const int n = n0 + (lane & 15) * 8;
+#pragma unroll 4
+            for (int q = 0; q < 16; ++q) {
+                const int row = wave * 64 + 4 * q + (lane >> 4);
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * kOutPitchHalf + (lane & 15) * 16);
+                const uint32_t off =
+                    (row < rows && n < F) ? ((uint32_t)row * (uint32_t)F + (uint32_t)n) * 2u : kOOR;
+                __builtin_amdgcn_raw_buffer_store_b128(v, cres, off, 0, 0);
+            }
+        } else {
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = 1.0f;
+                if constexpr (EPI == EPI_ROW_SCALE) {
+                    const int row = (wm * 4 + i) * 32 + r32;
+                    sc[i] = g.row_scale[s0 + min(row, rows - 1)];
                 }
-        }
-        __syncthreads();
-        const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * N, (short)0, rows * N * 2,
-                                                                               kBufDword3);
-        {
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitch;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            v[e] = EPI == EPI_ROW_SCALE ? sc[i] * acc[i][j][4 * r + e] : acc[i][j][4 * r + e];
+                        const int col = (wn * 4 + j) * 32 + 8 * r + 4 * kh;
+                        const u32x2_t val = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        *reinterpret_cast<u32x2_t*>(orow + col * 2) = val;
+                    }
+            }
+            __syncthreads();
+            const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * N, (short)0,
+                                                                                   rows * N * 2, kBufDword3);
             const int n = n0 + (lane & 31) * 8;
 #pragma unroll 4
             for (int q = 0; q < 32; ++q) {
@@ -396,7 +463,7 @@ using namespace et;
 
 extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
                               const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
-                              int64_t slot_capacity, void* c, void* stream)
+                              int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream)
 {
     const char* fn = "et_expert_gemm";
     const int64_t E = num_experts;
@@ -407,6 +474,10 @@ extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sort
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": K must be a positive multiple of 8 below 2^22");
     if (N < 8 || N % 8 != 0)
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N must be a positive multiple of 8");
+    if (epilogue != ET_GEMM_PLAIN && epilogue != ET_GEMM_ROW_SCALE && epilogue != ET_GEMM_SWIGLU)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": unknown epilogue " + std::to_string(epilogue));
+    if (epilogue == ET_GEMM_SWIGLU && N % 16 != 0)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": SwiGLU needs N = 2 F with F a multiple of 8");
     if (N * K * 2 >= (int64_t(1) << 31))
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": one expert's weight (N * K * 2 bytes) must be below 2 GiB");
     if (kBM * N * 2 >= (int64_t(1) << 31))
@@ -419,10 +490,12 @@ extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sort
                     std::string(fn) + ": in gather mode the token rows (a_rows * K * 2 bytes) must be below 2 GiB");
     if (slot_capacity == 0) return ET_OK;
     if (!a || !w || !expert_offsets || !c) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null pointer");
+    if (epilogue == ET_GEMM_ROW_SCALE && !row_scale)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": the row-scale epilogue needs row_scale");
     if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15) ||
-        (reinterpret_cast<uintptr_t>(c) & 7))
-        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": a and w must be 16-byte aligned, c 8-byte aligned");
-    const int64_t nN = (N + kBN - 1) / kBN;
+        (reinterpret_cast<uintptr_t>(c) & 15))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": a, w and c must be 16-byte aligned");
+    const int64_t nN = epilogue == ET_GEMM_SWIGLU ? (N / 2 + kBN / 2 - 1) / (kBN / 2) : (N + kBN - 1) / kBN;
     const int64_t qmax = ((slot_capacity + kBM - 1) / kBM + E) * nN;
     if (qmax >= (int64_t(1) << 31))
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": too many output tiles (slot_capacity / 256 * N / 256)");
@@ -430,8 +503,16 @@ extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sort
     const dim3 grid((unsigned)(8 * ((blocks + 7) / 8)));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const GemmArgs args{static_cast<const uint16_t*>(a), sorted_token, static_cast<const uint16_t*>(w),
-                        expert_offsets, static_cast<uint16_t*>(c), a_rows, slot_capacity, (int)K, (int)N, (int)E};
-    if (gather) expert_gemm_kernel<true><<<grid, dim3(kThreads), 0, s>>>(args);
-    else expert_gemm_kernel<false><<<grid, dim3(kThreads), 0, s>>>(args);
+                        expert_offsets, static_cast<uint16_t*>(c), row_scale, a_rows, slot_capacity,
+                        (int)K, (int)N, (int)E};
+    const dim3 block(kThreads);
+    switch (epilogue * 2 + (gather ? 1 : 0)) {
+        case 0: expert_gemm_kernel<false, EPI_PLAIN><<<grid, block, 0, s>>>(args); break;
+        case 1: expert_gemm_kernel<true, EPI_PLAIN><<<grid, block, 0, s>>>(args); break;
+        case 2: expert_gemm_kernel<false, EPI_ROW_SCALE><<<grid, block, 0, s>>>(args); break;
+        case 3: expert_gemm_kernel<true, EPI_ROW_SCALE><<<grid, block, 0, s>>>(args); break;
+        case 4: expert_gemm_kernel<false, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
+        default: expert_gemm_kernel<true, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
+    }
     return check_launch("expert_gemm_kernel");
 }

@@ -28,7 +28,8 @@ from typing import Optional
 
 import torch
 
-from ._lib import ET_DTYPE_BF16, ET_DTYPE_F32, ET_MAX_EXPERTS, ET_MAX_ROUTER_EXPERTS, check, lib
+from ._lib import (ET_DTYPE_BF16, ET_DTYPE_F32, ET_GEMM_PLAIN, ET_GEMM_ROW_SCALE, ET_GEMM_SWIGLU,
+                   ET_MAX_EXPERTS, ET_MAX_ROUTER_EXPERTS, check, lib)
 
 _ACT_DTYPES = {torch.float32: ET_DTYPE_F32, torch.bfloat16: ET_DTYPE_BF16}
 
@@ -351,22 +352,33 @@ def router_weight_grad(dlogits: torch.Tensor, x: torch.Tensor, out: Optional[tor
 # expert grouped GEMM
 # --------------------------------------------------------------------------- #
 
+_EPILOGUES = {"none": ET_GEMM_PLAIN, "row_scale": ET_GEMM_ROW_SCALE, "swiglu": ET_GEMM_SWIGLU}
+
+
 def expert_gemm(a: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: bool = True,
+                epilogue: str = "none", row_scale: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Grouped expert GEMM over the plan's slot blocks (bf16, binary32 accumulation).
 
-    out[s] = A[row(s)] @ W[e(s)]^T for every routed slot s, e(s) its expert.
+    p[s] = A[row(s)] @ W[e(s)]^T for every routed slot s, e(s) its expert, then
+    the epilogue, rounded once to bf16:
+      "none"       out[s] = p[s]                                   [rows, N]
+      "row_scale"  out[s] = row_scale[s] * p[s]  (e.g. slot_gate)  [rows, N]
+      "swiglu"     out[s, f] = silu(p[s, f]) * p[s, F + f], F = N/2 [rows, F]
+                   (W holds each expert's gate rows, then its up rows)
     gather=True: ``a`` is the token matrix X [T, K] and row(s) = the slot's token
     (the dispatch fused into the GEMM: Xp is never materialised).
     gather=False: ``a`` is slot-major [rows, K] (e.g. dispatch(X) or an
     activation of the previous projection) and row(s) = s.
-    ``w`` is [E, N, K], each expert's weight in nn.Linear layout.  Returns
-    [rows, N] bf16; rows of ``out`` past the routed slots are left as they were.
+    ``w`` is [E, N, K], each expert's weight in nn.Linear layout.  Rows of
+    ``out`` past the routed slots are left as they were.
     """
     _require(a, "a", torch.bfloat16, 2)
     dev = a.device
     _require(w, "w", torch.bfloat16, 3, dev)
     _check_plan(plan, dev)
+    if epilogue not in _EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(_EPILOGUES)}, got {epilogue!r}")
     E, N, K = w.shape
     if E != plan.num_experts:
         raise ValueError(f"w has {E} experts, plan has {plan.num_experts}")
@@ -374,8 +386,8 @@ def expert_gemm(a: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: 
         raise ValueError(f"a has row length {a.shape[1]}, w has K = {K}")
     if K < 8 or K % 8 or K >= 1 << 22:
         raise ValueError(f"K must be a positive multiple of 8 below 2^22, got {K}")
-    if N < 8 or N % 8:
-        raise ValueError(f"N must be a positive multiple of 8, got {N}")
+    if N < 8 or N % 8 or (epilogue == "swiglu" and N % 16):
+        raise ValueError(f"N must be a positive multiple of 8 (16 for swiglu), got {N}")
     if N * K * 2 >= 1 << 31:
         raise ValueError("one expert's weight must be below 2 GiB")
     if gather:
@@ -385,12 +397,20 @@ def expert_gemm(a: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: 
             raise ValueError("in gather mode the token matrix must be below 2 GiB")
     elif a.shape[0] != plan.rows:
         raise ValueError(f"a has {a.shape[0]} rows, plan has {plan.rows} slots")
-    c = _out_or_new(out, (plan.rows, N), torch.bfloat16, dev, "out")
-    if a.data_ptr() % 16 or w.data_ptr() % 16 or c.data_ptr() % 8:
-        raise ValueError("a and w must be 16-byte aligned, out 8-byte aligned")
+    if epilogue == "row_scale":
+        if row_scale is None:
+            raise ValueError("the row_scale epilogue needs row_scale")
+        _require(row_scale, "row_scale", torch.float32, 1, dev)
+        if row_scale.shape[0] < plan.rows:
+            raise ValueError(f"row_scale has {row_scale.shape[0]} entries, plan has {plan.rows} slots")
+    ncols = N // 2 if epilogue == "swiglu" else N
+    c = _out_or_new(out, (plan.rows, ncols), torch.bfloat16, dev, "out")
+    if a.data_ptr() % 16 or w.data_ptr() % 16 or c.data_ptr() % 16:
+        raise ValueError("a, w and out must be 16-byte aligned")
     with torch.cuda.device(dev):
         rc = lib().et_expert_gemm(_vp(a), a.shape[0], _vp(plan.sorted_token) if gather else None, _vp(w),
-                                  _vp(plan.expert_offsets), E, K, N, plan.rows, _vp(c), _stream(dev))
+                                  _vp(plan.expert_offsets), E, K, N, plan.rows, _EPILOGUES[epilogue],
+                                  _vp(row_scale) if epilogue == "row_scale" else None, _vp(c), _stream(dev))
     check("et_expert_gemm", rc)
     return c
 

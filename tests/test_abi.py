@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 4" in hdr
-    assert et.lib().et_abi_version() == 4
+    assert "#define ET_ABI_VERSION 5" in hdr
+    assert et.lib().et_abi_version() == 5
 
 
 def test_workspace_sizes(et):
@@ -133,22 +133,31 @@ def test_router_logits_rejects_bad_arguments(et):
 def test_expert_gemm_rejects_bad_arguments(et):
     lib = et.lib()
     p = ctypes.c_void_p(0x1000)
-    # (a, a_rows, sorted_token, w, expert_offsets, E, K, N, slot_capacity, c, stream)
-    assert lib.et_expert_gemm(p, 16, p, p, p, 0, 64, 64, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    # (a, a_rows, sorted_token, w, expert_offsets, E, K, N, slot_capacity, epilogue, row_scale, c, stream)
+    assert lib.et_expert_gemm(p, 16, p, p, p, 0, 64, 64, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "num_experts" in _err(et)
-    assert lib.et_expert_gemm(p, 16, p, p, p, 1025, 64, 64, 16, p, None) == ET_ERR_INVALID_ARGUMENT
-    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 60, 64, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 16, p, p, p, 1025, 64, 64, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 60, 64, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "K must" in _err(et)
-    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 12, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 12, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "N must" in _err(et)
-    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 1 << 16, 1 << 14, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, 16, 3, None, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "epilogue" in _err(et)
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 24, 16, 2, None, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "SwiGLU" in _err(et)
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, 16, 1, None, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "row_scale" in _err(et)
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 1 << 16, 1 << 14, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "2 GiB" in _err(et)
-    assert lib.et_expert_gemm(p, 1 << 20, p, p, p, 4, 4096, 64, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 1 << 20, p, p, p, 4, 4096, 64, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "gather" in _err(et)
-    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, -1, p, None) == ET_ERR_INVALID_ARGUMENT
-    assert lib.et_expert_gemm(p, 16, p, p, None, 4, 64, 64, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, -1, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(p, 16, p, p, None, 4, 64, 64, 16, 0, None, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "null" in _err(et)
-    assert lib.et_expert_gemm(ctypes.c_void_p(0x1008), 16, p, p, p, 4, 64, 64, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm(ctypes.c_void_p(0x1008), 16, p, p, p, 4, 64, 64, 16, 0, None, p, None) \
+        == ET_ERR_INVALID_ARGUMENT
     assert "aligned" in _err(et)
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, 16, 0, None, ctypes.c_void_p(0x1008), None) \
+        == ET_ERR_INVALID_ARGUMENT
     # no slot rows: nothing to do, nothing launched
-    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, 0, p, None) == 0
+    assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, 0, 0, None, p, None) == 0

@@ -17,7 +17,11 @@ formula):
   * random inputs stay within the binary32 summation bound K * 2^-24 *
     sum_k |a_k w_k| of the float64 product plus one bf16 rounding;
   * rows past the routed slots are left untouched, and an undersized slot
-    capacity computes exactly the slots below it.
+    capacity computes exactly the slots below it;
+  * the epilogues on exact integer products: SwiGLU equals the CPU oracle's
+    binary32 (g * sigmoid(g)) * u (oracle_swiglu, itself pinned against
+    float64) rounded to bf16, bit for bit; the row scale equals torch's float64
+    product rounded to binary32 and then bf16.
 """
 import pytest
 import torch
@@ -163,3 +167,67 @@ def test_expert_gemm_c3_shape(et, dev):
         err = (c[sample[sel]].double() - ref).abs()
         acc_bound = K * 2.0 ** -24 * mass
         assert bool((err <= 2.0 ** -8 * (ref.abs() + acc_bound) + acc_bound).all()), e
+
+
+SWIGLU_SHAPES = [  # (T, K, F, E, k, skew): F off the 128-unit tile, one expert, many tiles per expert
+    (1, 8, 8, 1, 1, 0.0), (300, 40, 200, 5, 2, 0.0), (1000, 256, 136, 8, 3, 0.0),
+    (2000, 64, 1536, 16, 4, 0.0), (5000, 128, 256, 64, 4, 12.0),
+]
+
+
+@pytest.mark.parametrize("T,K,F,E,k,skew", SWIGLU_SHAPES)
+def test_expert_gemm_swiglu_exact_on_integer_inputs(et, orc, dev, T, K, F, E, k, skew):
+    """Integer inputs make the gate and up products exact, so every output must
+    be the oracle's binary32 (g * sigmoid(g)) * u of them, rounded once to bf16."""
+    import numpy as np
+    print(f"expert_gemm swiglu T={T} K={K} F={F} E={E}", flush=True)
+    plan = _plan(et, dev, T, E, k, seed=T * 7 + F, skew=skew)
+    g = torch.Generator(device=dev)
+    g.manual_seed(K * 5 + F)
+    x = _int_bf16((T, K), g, dev, lim=1)
+    w = _int_bf16((E, 2 * F, K), g, dev, lim=1)
+    S = plan.num_slots
+    p, _ = _reference(x, w, plan, S)                     # exact: |sums| <= K
+    gate, up = p[:, :F].float().cpu().numpy(), p[:, F:].float().cpu().numpy()
+    want = orc.f32_to_bf16(orc.swiglu(gate, up)).view(np.int16)
+    for gather in (True, False):
+        a = x if gather else et.dispatch(x, plan)
+        h = et.expert_gemm(a, w, plan, gather=gather, epilogue="swiglu")
+        assert tuple(h.shape) == (S, F)
+        assert np.array_equal(_bits(h).cpu().numpy(), want)
+
+
+def test_expert_gemm_row_scale_exact_on_integer_inputs(et, dev):
+    """A per-slot factor (the slot gate) times an exact integer product rounds
+    once to binary32 and once to bf16, as torch's float64 -> f32 -> bf16 does."""
+    T, K, N, E = 3000, 136, 520, 12
+    plan = _plan(et, dev, T, E, 3, seed=21)
+    g = torch.Generator(device=dev)
+    g.manual_seed(22)
+    x = _int_bf16((T, K), g, dev)
+    w = _int_bf16((E, N, K), g, dev)
+    S = plan.num_slots
+    ref, _ = _reference(x, w, plan, S)
+    want = (ref * plan.slot_gate.double()[:, None]).float().to(torch.bfloat16)
+    for gather in (True, False):
+        a = x if gather else et.dispatch(x, plan)
+        c = et.expert_gemm(a, w, plan, gather=gather, epilogue="row_scale", row_scale=plan.slot_gate)
+        assert torch.equal(_bits(c), _bits(want))
+
+
+def test_expert_gemm_swiglu_random(et, dev):
+    """Random inputs: within the bf16 bar of float64 silu(g) * u."""
+    T, K, F, E = 4096, 2048, 768, 16
+    plan = _plan(et, dev, T, E, 4, seed=31)
+    g = torch.Generator(device=dev)
+    g.manual_seed(32)
+    x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(E, 2 * F, K, generator=g, device=dev) * K ** -0.5).to(torch.bfloat16)
+    h = et.expert_gemm(x, w, plan, epilogue="swiglu")
+    h2 = et.expert_gemm(x, w, plan, epilogue="swiglu")
+    assert torch.equal(_bits(h), _bits(h2))
+    p, _ = _reference(x, w, plan, plan.num_slots)
+    gate, up = p[:, :F], p[:, F:]
+    want = gate * torch.sigmoid(gate) * up
+    err = (h.double() - want).abs()
+    assert bool((err <= 1e-2 * want.abs() + 1e-3 * want.pow(2).mean().sqrt()).all())

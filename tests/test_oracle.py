@@ -69,6 +69,25 @@ def test_sigmoid_within_two_ulp_and_monotone(orc):
     assert np.all(np.diff(got[order]) >= 0)
 
 
+def test_swiglu_within_a_few_ulp_of_float64(orc):
+    """oracle_swiglu = (g * sigmoid(g)) * u: three binary32 roundings on top of
+    the sigmoid's 2 ulp, so within ~5 ulp of float64 silu(g) * u away from
+    underflow; exact at g = 0 (0), u = 0 (signed 0) and g = +inf (u * inf)."""
+    rng = np.random.default_rng(7)
+    g = np.concatenate([np.linspace(-30.0, 30.0, 6001), rng.standard_normal(4000) * 3]).astype(np.float32)
+    u = (rng.standard_normal(g.size) * 2).astype(np.float32)
+    got = orc.swiglu(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    ref = (g64 / (1.0 + np.exp(-g64)) * u64).astype(np.float32)
+    big = np.abs(ref) > 1e-30
+    assert ulp_diff(got[big], ref[big]).max() <= 5
+    assert orc.swiglu(np.float32([0.0]), np.float32([3.0]))[0] == 0.0
+    assert orc.swiglu(np.float32([2.0]), np.float32([0.0]))[0] == 0.0
+    assert orc.swiglu(np.float32([np.inf]), np.float32([2.0]))[0] == np.inf
+    # a transposed or dropped factor fails: silu(u) * g != silu(g) * u
+    assert not np.array_equal(orc.swiglu(u, g), got)
+
+
 def test_sigmoid_is_monotone_up_to_two_order_steps_over_all_floats(orc):
     """Exhaustive over all 2^32 bit patterns (NaN logits skipped): the
     specified sigmoid never returns a negative score, and each score is at most
