@@ -283,6 +283,34 @@ int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, c
                    const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
                    int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream);
 
+/*
+ * Weight transpose for the expert GEMM's input gradient:
+ *   wt[e, k, n] = w[e, n, k]   (bf16, exact copies)
+ * for every expert with at least one slot below slot_capacity (the others are
+ * left as they were).  With it, dA = dC . W_e -- the input gradient of
+ * c = a . W_e^T -- is et_expert_gemm(dC, wt) (K' = N, N' = K).  N and K
+ * multiples of 8, N*K below 2^31; w and wt 16-byte aligned, not aliased.
+ * Implements the layout change the expert GEMM's backward needs (no reference
+ * counterpart).
+ */
+int et_expert_weight_transpose(const void* w, const int32_t* expert_offsets, int64_t num_experts,
+                               int64_t N, int64_t K, int64_t slot_capacity, void* wt, void* stream);
+
+/*
+ * Weight gradient of the expert GEMM:
+ *   dw[e, n, k] = sum over e's slots s (s < slot_capacity) of dc[s, n] * a[s, k]
+ * dc bf16 [slot_capacity, N] (the gradient of c), a bf16 [slot_capacity, K]
+ * slot-major (the operand of the forward product; dispatch(X) for a gathered
+ * forward), dw f32 [E, N, K]; experts without slots get zeros.  Binary32
+ * accumulation on the matrix cores over the slots in ascending order, in steps
+ * of 16 (one MFMA each): repeated calls give identical bits, and integer-valued
+ * inputs whose partial sums stay below 2^24 give the exact result.  N and K
+ * multiples of 8, N*K*4 below 2^31 bytes; dc and a 16-byte aligned.
+ * Implements the expert GEMM's weight gradient (no reference counterpart).
+ */
+int et_expert_wgrad(const void* dc, const void* a, const int32_t* expert_offsets, int64_t num_experts,
+                    int64_t N, int64_t K, int64_t slot_capacity, float* dw, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,9 @@ from .expert_threshold import (  # noqa: F401
     dispatch_autograd,
     dispatch_backward,
     expert_gemm,
+    expert_gemm_input_grad,
+    expert_gemm_weight_grad,
+    expert_weight_transpose,
     route,
     route_workspace_bytes,
     router_logits,

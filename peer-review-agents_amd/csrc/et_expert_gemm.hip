@@ -368,7 +368,8 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             // h = (g * sigmoid(g)) * u in binary32, from the gate tiles j = 0, 1
             // and the up tiles j + 2 of the same lane and register; 128 hidden
             // columns per tile, wave column half wn holds hidden wn * 64 ...
-#pragma unroll
+            // (one slot tile at a time keeps the sigmoid temporaries few)
+#pragma unroll 1
             for (int i = 0; i < 4; ++i) {
                 unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitchHalf;
 #pragma unroll
@@ -399,6 +400,9 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                 __builtin_amdgcn_raw_buffer_store_b128(v, cres, off, 0, 0);
             }
         } else {
+            // (the compiler barrier keeps the row-scale loads here rather than
+            // hoisted above the K loop, where their registers would be live)
+            asm volatile("" ::: "memory");
             float sc[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -410,6 +414,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if constexpr (EPI == EPI_ROW_SCALE) __builtin_amdgcn_sched_barrier(0);   // one slot tile at a time
                 unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitch;
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -515,4 +520,308 @@ extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sort
         default: expert_gemm_kernel<true, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
     }
     return check_launch("expert_gemm_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Weight transpose for the input gradient: wt[e, k, n] = w[e, n, k] for the
+// experts with slots, so that dA = dC . W_e is a product against wt in the
+// layout the grouped GEMM above reads (nn.Linear: rows are output features).
+// ---------------------------------------------------------------------------
+
+namespace et {
+namespace {
+
+constexpr int kTrTile = 64;
+
+// Block (x, y) owns the 64 x 64 tile (k0 = 64 x, n0 = 64 y) of every expert
+// z, z + gridDim.z, ...; experts without slots are skipped.  Rows are read and
+// written 16 bytes per thread (N and K are multiples of 8); the tile passes
+// through LDS with rows padded by 16 bytes.
+__global__ __launch_bounds__(256) void weight_transpose_kernel(const uint16_t* __restrict__ w,
+                                                                uint16_t* __restrict__ wt,
+                                                                const int32_t* __restrict__ expert_offsets, int E,
+                                                                int N, int K, int64_t cap)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kTrTile][kTrTile + 8];
+    const int tid = threadIdx.x;
+    const int k0 = blockIdx.x * kTrTile, n0 = blockIdx.y * kTrTile;
+    const int r = tid >> 3, c8 = (tid & 7) * 8;
+    for (int e = blockIdx.z; e < E; e += gridDim.z) {
+        const int64_t lo = min<int64_t>(expert_offsets[e], cap);
+        const int64_t hi = min<int64_t>(expert_offsets[e + 1], cap);
+        if (hi <= lo) continue;                       // block-uniform
+        const uint16_t* src = w + (int64_t)e * N * K;
+        uint16_t* dst = wt + (int64_t)e * N * K;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int n = n0 + r + 32 * p, k = k0 + c8;
+            u32x4_t v = {0u, 0u, 0u, 0u};
+            if (n < N && k < K) v = *reinterpret_cast<const u32x4_t*>(src + (int64_t)n * K + k);
+            *reinterpret_cast<u32x4_t*>(&tile[r + 32 * p][c8]) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int k = k0 + r + 32 * p, n = n0 + c8;
+            uint32_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                q[i] = (uint32_t)tile[c8 + 2 * i][r + 32 * p] | ((uint32_t)tile[c8 + 2 * i + 1][r + 32 * p] << 16);
+            if (k < K && n < N) *reinterpret_cast<u32x4_t*>(dst + (int64_t)k * N + n) = u32x4_t{q[0], q[1], q[2], q[3]};
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+}  // namespace et
+
+extern "C" int et_expert_weight_transpose(const void* w, const int32_t* expert_offsets, int64_t num_experts,
+                                          int64_t N, int64_t K, int64_t slot_capacity, void* wt, void* stream)
+{
+    const char* fn = "et_expert_weight_transpose";
+    if (num_experts < 1 || num_experts > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_EXPERTS) + "]");
+    if (N < 8 || N % 8 != 0 || K < 8 || K % 8 != 0 || N * K >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N and K must be positive multiples of 8, N*K < 2^31");
+    if (slot_capacity < 0) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": slot_capacity < 0");
+    if (!w || !expert_offsets || !wt) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null pointer");
+    if ((reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(wt) & 15))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": w and wt must be 16-byte aligned");
+    if (w == wt) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": w and wt must not alias");
+    const dim3 grid((unsigned)((K + kTrTile - 1) / kTrTile), (unsigned)((N + kTrTile - 1) / kTrTile),
+                    (unsigned)std::min<int64_t>(num_experts, 16));
+    weight_transpose_kernel<<<grid, dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t*>(w), static_cast<uint16_t*>(wt), expert_offsets, (int)num_experts, (int)N,
+        (int)K, slot_capacity);
+    return check_launch("weight_transpose_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Weight gradient of the expert GEMM:
+//   dw[e, n, k] = sum over e's slots s of dc[s, n] * a[s, k]      (f32 out)
+// with dc [cap, N] and a [cap, K] slot-major bf16.  The sum runs over the
+// slot (row) dimension of both operands, so neither loads as an MFMA fragment
+// directly: a stage holds each operand's 64-slot chunk row-major (64 rows x
+// 256 columns x 2 bytes), and the fragments -- 8 consecutive slots of one
+// column per lane -- come from gfx950's transposing LDS read
+// ds_read_b64_tr_b16.  Within each 16-lane group, if lane j points at 4
+// consecutive 16-bit elements M[j][0..3], lane i receives M[4 m + i / 4][i % 4]
+// for m = 0..3 (checked on the device).  So with lane j pointing at row
+// r0 + j / 4, columns c0 + 4 (j % 4), lane i gets column c0 + i of rows
+// r0..r0+3: two such reads give an MFMA operand of 8 consecutive slots.
+// Each 512-byte row stores its 16-byte segment s at slot s ^ (4 (row & 3)),
+// which puts the four rows of one read on distinct 64-byte bank windows.
+// The product is issued as mfma(dc fragment, a fragment): lane l holds column
+// k = l % 32 of a tile and rows n = 8 (r / 4) + 4 (l / 32) + r % 4, stored as
+// 128-byte row pieces.
+// ---------------------------------------------------------------------------
+
+namespace et {
+namespace {
+
+struct WgradArgs {
+    const uint16_t* dc;             // [cap, N]
+    const uint16_t* a;              // [cap, K]
+    const int32_t* expert_offsets;  // [E + 1]
+    float* dw;                      // [E, N, K]
+    int64_t cap;
+    int K, N, E;
+};
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+__device__ __forceinline__ uint2 read_tr16(const unsigned char* p)
+{
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4_t*)(__attribute__((address_space(3))) unsigned char*)p);
+    return __builtin_bit_cast(uint2, v);
+}
+
+__global__ __launch_bounds__(kThreads) void expert_wgrad_kernel(WgradArgs g)
+{
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kStage];
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int E = g.E, K = g.K, N = g.N;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nNt = (N + kBN - 1) / kBN, nKt = (K + kBN - 1) / kBN;
+    const int Q = E * nNt * nKt;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
+
+    // Direct loads of a chunk: wave w fills row pairs 8 w + i (i < 8) of each
+    // operand, rows r = 16 w + 2 i + lane / 32, 16-byte slot q = lane % 32,
+    // holding column segment q ^ (4 (r & 3)).
+    // Fragment reads (tile t of 32 columns, k-step ks of 16 slots, half h):
+    // lane l reads row 16 ks + 8 (l / 32) + 4 h + j / 4 (j = l % 16), columns
+    // 32 t + 16 ((l / 16) % 2) + 4 (j % 4) .. + 3.
+    // Per-lane LDS offset of tile t's fragment at k-step 0, half 0; k-step ks
+    // and half h add (16 ks + 4 h) * 512 bytes (the row & 3 of the swizzle is
+    // j / 4 for every ks and h).
+    const int jj = lane & 15;
+    uint32_t fb[2][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int o = 0; o < 2; ++o) {
+            const int tile = (o == 0 ? wm : wn) * 4 + t;
+            const int seg = 4 * tile + 2 * ((lane >> 4) & 1) + ((jj & 3) >> 1);
+            const int slot = seg ^ (4 * (jj >> 2));
+            fb[o][t] = (uint32_t)((8 * (lane >> 5) + (jj >> 2)) * 512 + slot * 16 + (jj & 1) * 8 + o * kHalf);
+        }
+    }
+
+    for (int q = blockIdx.x; q < Q; q += gridDim.x) {
+        const int e = q / (nNt * nKt);
+        const int rem = q - e * nNt * nKt;
+        const int n0 = (rem / nKt) * kBN, k0 = (rem % nKt) * kBN;
+        const int64_t lo = min<int64_t>(g.expert_offsets[e], g.cap);
+        const int64_t hi = min<int64_t>(g.expert_offsets[e + 1], g.cap);
+        const int se = (int)max<int64_t>(0, hi - lo);
+        const int nk = (se + 63) / 64;
+
+        uint32_t doff[8], aoff[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 16 * wave + 2 * i + (lane >> 5);
+            const int seg = (lane & 31) ^ (4 * (r & 3));
+            const int n = n0 + 8 * seg, k = k0 + 8 * seg;
+            doff[i] = n < N ? ((uint32_t)r * (uint32_t)N + (uint32_t)n) * 2u : kOOR;
+            aoff[i] = k < K ? ((uint32_t)r * (uint32_t)K + (uint32_t)k) * 2u : kOOR;
+        }
+        // chunk c: slots lo + 64 c ..; descriptors rebased per chunk, so slots
+        // past the expert's read 0
+        auto issue = [&](int c) {
+            const int64_t s0 = lo + 64 * (int64_t)c;
+            const int nrow = min(64, (int)(hi - s0));
+            const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(g.dc + s0 * N), (short)0, nrow * N * 2, kBufDword3);
+            const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(g.a + s0 * K), (short)0, nrow * K * 2, kBufDword3);
+            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                dma_b128(dres, doff[i], 0u, sb + i * 1024);
+                dma_b128(ares, aoff[i], 0u, sb + kHalf + i * 1024);
+            }
+        };
+
+        f32x16_t acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+
+        u32x4_t f[4][2][4];       // [k-step][dc, a][tile]
+        auto read_frags = [&](int c, int ks) {
+            const unsigned char* st = smem + (c & 1) * kStage + ks * 16 * 512;
+#pragma unroll
+            for (int o = 0; o < 2; ++o)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint2 h0 = read_tr16(st + fb[o][t]);
+                    const uint2 h1 = read_tr16(st + fb[o][t] + 4 * 512);
+                    f[ks][o][t] = u32x4_t{h0.x, h0.y, h1.x, h1.y};
+                }
+        };
+        auto mfmas = [&](int ks) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][0][i]),
+                                                                        __builtin_bit_cast(bf16x8_t, f[ks][1][j]),
+                                                                        acc[i][j], 0, 0, 0);
+        };
+        auto barrier = [&]() {
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        };
+
+        // Same schedule as the forward kernel: a whole chunk's fragments in
+        // registers, two chunks streaming while one is multiplied.
+        barrier();
+        if (nk > 0) {
+            issue(0);
+            if (nk > 1) issue(1);
+            if (nk > 1) dma_wait_barrier<16>();
+            else dma_wait_barrier<0>();
+            read_frags(0, 0);
+            read_frags(0, 1);
+            read_frags(0, 2);
+        }
+        for (int c = 0; c < nk; ++c) {
+            read_frags(c, 3);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            barrier();
+            if (c + 2 < nk) issue(c + 2);
+            mfmas(1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(2);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 < nk) {
+                if (c + 2 < nk) dma_wait_barrier<16>();
+                else dma_wait_barrier<0>();
+                read_frags(c + 1, 0);
+                read_frags(c + 1, 1);
+                read_frags(c + 1, 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // Epilogue: f32 straight from the accumulators, 128-byte row pieces.
+        const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+            g.dw + (int64_t)e * N * K, (short)0, N * K * 4, kBufDword3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = k0 + (wn * 4 + j) * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int n = n0 + (wm * 4 + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    const uint32_t off = (n < N && k < K) ? ((uint32_t)n * (uint32_t)K + (uint32_t)k) * 4u : kOOR;
+                    __builtin_amdgcn_raw_buffer_store_b32(f2u(acc[i][j][r]), wres, off, 0, 0);
+                }
+            }
+    }
+}
+
+}  // namespace
+}  // namespace et
+
+extern "C" int et_expert_wgrad(const void* dc, const void* a, const int32_t* expert_offsets, int64_t num_experts,
+                               int64_t N, int64_t K, int64_t slot_capacity, float* dw, void* stream)
+{
+    const char* fn = "et_expert_wgrad";
+    if (num_experts < 1 || num_experts > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_EXPERTS) + "]");
+    if (N < 8 || N % 8 != 0 || K < 8 || K % 8 != 0)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N and K must be positive multiples of 8");
+    if (N * K * 4 >= (int64_t(1) << 31) || 64 * std::max(N, K) * 2 >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": one expert's gradient (N * K * 4 bytes) must be below 2 GiB");
+    if (slot_capacity < 0 || slot_capacity >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": slot_capacity out of range");
+    if (!expert_offsets || !dw || (slot_capacity > 0 && (!dc || !a)))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null pointer");
+    if ((reinterpret_cast<uintptr_t>(dc) & 15) || (reinterpret_cast<uintptr_t>(a) & 15) ||
+        (reinterpret_cast<uintptr_t>(dw) & 3))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": dc and a must be 16-byte aligned, dw 4-byte aligned");
+    const int64_t tiles = num_experts * ((N + kBN - 1) / kBN) * ((K + kBN - 1) / kBN);
+    if (tiles >= (int64_t(1) << 31)) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": too many tiles");
+    const dim3 grid((unsigned)std::min<int64_t>((int64_t)num_cus(), tiles));
+    const WgradArgs args{static_cast<const uint16_t*>(dc), static_cast<const uint16_t*>(a), expert_offsets, dw,
+                         slot_capacity, (int)K, (int)N, (int)num_experts};
+    expert_wgrad_kernel<<<grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(args);
+    return check_launch("expert_wgrad_kernel");
 }

@@ -415,6 +415,66 @@ def expert_gemm(a: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: 
     return c
 
 
+def expert_weight_transpose(w: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """wt[e] = w[e]^T ([E, K, N] bf16) for the plan's experts with slots (the
+    other experts' blocks of ``out`` are left as they were)."""
+    _require(w, "w", torch.bfloat16, 3)
+    dev = w.device
+    _check_plan(plan, dev)
+    E, N, K = w.shape
+    if E != plan.num_experts:
+        raise ValueError(f"w has {E} experts, plan has {plan.num_experts}")
+    if N % 8 or K % 8 or N * K >= 1 << 31:
+        raise ValueError("N and K must be multiples of 8 with N * K < 2^31")
+    wt = _out_or_new(out, (E, K, N), torch.bfloat16, dev, "out")
+    with torch.cuda.device(dev):
+        rc = lib().et_expert_weight_transpose(_vp(w), _vp(plan.expert_offsets), E, N, K, plan.rows, _vp(wt),
+                                              _stream(dev))
+    check("et_expert_weight_transpose", rc)
+    return wt
+
+
+def expert_gemm_input_grad(dc: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: bool = False,
+                           row_scale: Optional[torch.Tensor] = None, wt: Optional[torch.Tensor] = None,
+                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Input gradient of :func:`expert_gemm`: da[s] = dC[row(s)] @ W[e(s)]
+    ([rows, K] bf16), through the transposed weights of the experts with slots
+    and the grouped GEMM.
+
+    gather=True takes dC from a token matrix [T, N] at row(s) = token(s), and
+    ``row_scale`` multiplies each slot's row: with dC = dY and row_scale =
+    slot_gate this is the backward of the down projection fused with the
+    combine backward (dYp = gate * dY[token] is never written).
+    """
+    wt = expert_weight_transpose(w, plan, out=wt)
+    return expert_gemm(dc, wt, plan, gather=gather, epilogue="row_scale" if row_scale is not None else "none",
+                       row_scale=row_scale, out=out)
+
+
+def expert_gemm_weight_grad(dc: torch.Tensor, a: torch.Tensor, plan: RoutingPlan,
+                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Weight gradient of :func:`expert_gemm`: dw[e] = dC_e^T @ A_e over e's
+    slots (f32 [E, N, K]; zeros for experts without slots).  dc [rows, N] and
+    a [rows, K] are slot-major bf16 (a = dispatch(X) for a gathered forward)."""
+    _require(dc, "dc", torch.bfloat16, 2)
+    dev = dc.device
+    _require(a, "a", torch.bfloat16, 2, dev)
+    _check_plan(plan, dev)
+    if dc.shape[0] != plan.rows or a.shape[0] != plan.rows:
+        raise ValueError(f"dc and a must have {plan.rows} rows")
+    N, K, E = dc.shape[1], a.shape[1], plan.num_experts
+    if N % 8 or K % 8 or N * K * 4 >= 1 << 31:
+        raise ValueError("N and K must be multiples of 8 with N * K * 4 < 2^31")
+    dw = _out_or_new(out, (E, N, K), torch.float32, dev, "out")
+    if dc.data_ptr() % 16 or a.data_ptr() % 16:
+        raise ValueError("dc and a must be 16-byte aligned")
+    with torch.cuda.device(dev):
+        rc = lib().et_expert_wgrad(_vp(dc), _vp(a), _vp(plan.expert_offsets), E, N, K, plan.rows, _vp(dw),
+                                   _stream(dev))
+    check("et_expert_wgrad", rc)
+    return dw
+
+
 # --------------------------------------------------------------------------- #
 # EMA threshold update
 # --------------------------------------------------------------------------- #

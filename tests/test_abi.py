@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 19
+    assert len(syms) == 21
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name

@@ -231,3 +231,106 @@ def test_expert_gemm_swiglu_random(et, dev):
     want = gate * torch.sigmoid(gate) * up
     err = (h.double() - want).abs()
     assert bool((err <= 1e-2 * want.abs() + 1e-3 * want.pow(2).mean().sqrt()).all())
+
+
+# ---------------------------------------------------------------------------
+# backward: weight transpose, input gradient (plain and fused with the combine
+# backward), weight gradient
+# ---------------------------------------------------------------------------
+
+def _active(plan, rows):
+    eo = plan.expert_offsets.cpu().tolist()
+    return [e for e in range(plan.num_experts) if min(eo[e + 1], rows) > min(eo[e], rows)]
+
+
+def test_expert_weight_transpose(et, dev):
+    T, E, N, K = 2000, 12, 136, 520
+    plan = _plan(et, dev, T, E, 2, seed=41)
+    w = torch.randn(E, N, K, device=dev).to(torch.bfloat16)
+    out = torch.full((E, K, N), 7777, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    et.expert_weight_transpose(w, plan, out=out)
+    act = set(_active(plan, plan.rows))
+    for e in range(E):
+        if e in act:
+            assert torch.equal(_bits(out[e]), _bits(w[e].t().contiguous())), e
+        else:
+            assert bool((_bits(out[e]) == 7777).all()), e
+
+
+@pytest.mark.parametrize("T,N,K,E,k", [(300, 40, 200, 5, 2), (2000, 264, 1032, 16, 3), (777, 8, 64, 3, 1)])
+def test_expert_gemm_input_grad_exact(et, dev, T, N, K, E, k):
+    """da[s] = dc[s] @ W[e(s)] on integer inputs is exact; the fused form
+    (dc gathered from a token matrix, each row times the slot gate) equals
+    gate * (dY[token] @ W) rounded once to binary32 and once to bf16."""
+    print(f"expert_gemm input grad T={T} N={N} K={K} E={E}", flush=True)
+    plan = _plan(et, dev, T, E, k, seed=T + N)
+    g = torch.Generator(device=dev)
+    g.manual_seed(N * 3 + K)
+    S = plan.num_slots
+    w = _int_bf16((E, N, K), g, dev)                    # forward weight [E, N, K]: c = a @ W^T
+    dc = _int_bf16((S, N), g, dev)
+    da = et.expert_gemm_input_grad(dc, w, plan)
+    wt = torch.stack([w[e].t() for e in range(E)]).contiguous()   # [E, K, N]
+    ref, _ = _reference(dc, wt, plan, S, gather=False)
+    assert torch.equal(_bits(da), _bits(ref.float().to(torch.bfloat16)))
+    dy = _int_bf16((T, N), g, dev)
+    fused = et.expert_gemm_input_grad(dy, w, plan, gather=True, row_scale=plan.slot_gate)
+    ref2, _ = _reference(dy, wt, plan, S, gather=True)
+    want = (ref2 * plan.slot_gate.double()[:, None]).float().to(torch.bfloat16)
+    assert torch.equal(_bits(fused), _bits(want))
+
+
+WGRAD_SHAPES = [  # (T, N, K, E, k, skew): N, K off the 256-wide tiles; experts without slots; an expert
+    # over many 64-slot chunks with a partial last one
+    (1, 8, 8, 1, 1, 0.0), (300, 40, 200, 5, 2, 0.0), (1000, 264, 136, 8, 3, 0.0),
+    (2000, 64, 520, 24, 2, 0.0), (5000, 128, 256, 16, 2, 12.0),
+]
+
+
+@pytest.mark.parametrize("T,N,K,E,k,skew", WGRAD_SHAPES)
+def test_expert_gemm_weight_grad_exact(et, dev, T, N, K, E, k, skew):
+    """dw[e] = dc_e^T @ a_e on integer inputs whose sums stay below 2^24 is
+    exact in binary32; experts without slots get zeros."""
+    print(f"expert_gemm weight grad T={T} N={N} K={K} E={E}", flush=True)
+    plan = _plan(et, dev, T, E, k, seed=T * 3 + K, skew=skew)
+    g = torch.Generator(device=dev)
+    g.manual_seed(N + 7 * K)
+    S = plan.num_slots
+    dc = _int_bf16((S, N), g, dev, lim=2)
+    a = _int_bf16((S, K), g, dev, lim=2)
+    dw = et.expert_gemm_weight_grad(dc, a, plan)
+    eo = plan.expert_offsets.cpu().tolist()
+    for e in range(E):
+        lo, hi = eo[e], eo[e + 1]
+        want = dc[lo:hi].double().t() @ a[lo:hi].double() if hi > lo else torch.zeros(N, K, device=dev,
+                                                                                        dtype=torch.float64)
+        assert torch.equal(dw[e].double(), want), e
+    assert torch.equal(dw, et.expert_gemm_weight_grad(dc, a, plan))
+
+
+def test_expert_gemm_weight_grad_random_and_capacity(et, dev):
+    T, N, K, E = 4096, 512, 768, 8
+    plan = _plan(et, dev, T, E, 2, seed=51)
+    S = plan.num_slots
+    g = torch.Generator(device=dev)
+    g.manual_seed(52)
+    dc = torch.randn(S, N, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(S, K, generator=g, device=dev).to(torch.bfloat16)
+    dw = et.expert_gemm_weight_grad(dc, a, plan)
+    eo = plan.expert_offsets.cpu().tolist()
+    for e in range(E):
+        lo, hi = eo[e], eo[e + 1]
+        d64, a64 = dc[lo:hi].double(), a[lo:hi].double()
+        want = d64.t() @ a64
+        mass = d64.abs().t() @ a64.abs()
+        assert bool(((dw[e].double() - want).abs() <= max(hi - lo, 1) * 2.0 ** -24 * mass).all()), e
+    # an undersized capacity sums the slots below it only
+    cap = S - 300
+    plan_c = _plan(et, dev, T, E, 2, seed=51, slot_capacity=cap)
+    dw_c = et.expert_gemm_weight_grad(dc[:cap].contiguous(), a[:cap].contiguous(), plan_c)
+    for e in range(E):
+        lo, hi = min(eo[e], cap), min(eo[e + 1], cap)
+        want = dc[lo:hi].double().t() @ a[lo:hi].double() if hi > lo else torch.zeros(N, K, device=dev,
+                                                                                        dtype=torch.float64)
+        mass = dc[lo:hi].double().abs().t() @ a[lo:hi].double().abs() if hi > lo else want
+        assert bool(((dw_c[e].double() - want).abs() <= max(hi - lo, 1) * 2.0 ** -24 * mass).all()), e
