@@ -232,7 +232,9 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     operand load, and the down projection (K = EXPERT_FFN, N = d) on a
     slot-major operand, each against torch's grouped GEMM (hipBLASLt) -- which
     needs the dispatched Xp, so the dispatch is timed beside it.  The gate/up
-    projection is also timed with the SwiGLU epilogue (half the output).  Random-init
+    projection is also timed with the SwiGLU epilogue (half the output), and
+    the backward of both projections: the input gradients (the down one fused
+    with the combine backward) and the f32 weight gradients.  Random-init
     expert weights of that shape; measured after the timed step with HIP events
     on the stream the kernels run on."""
     import torch
@@ -269,7 +271,33 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     t_up_lib = timed(lambda: torch._grouped_mm(xp, w1t, offs=offs))
     t_down_lib = timed(lambda: torch._grouped_mm(a2, w2t, offs=offs))
     fl_up, fl_down = 2.0 * S * d * 2 * F, 2.0 * S * F * d
-    del w1, w2, h, a2, y, xp
+    # backward: the down projection's input gradient fused with the combine
+    # backward (dY gathered, rows times the slot gate), the gate/up
+    # projection's input gradient (both through the transposed weights of the
+    # experts with slots), and both weight gradients (f32)
+    dy = torch.randn(T, d, device=dev, generator=g).to(torch.bfloat16)
+    dgu = torch.randn(S, 2 * F, device=dev, generator=g).to(torch.bfloat16)
+    w2t = torch.empty(E, F, d, dtype=torch.bfloat16, device=dev)
+    w1t = torch.empty(E, d, 2 * F, dtype=torch.bfloat16, device=dev)
+    dh = torch.empty(S, F, dtype=torch.bfloat16, device=dev)
+    dxp = torch.empty(S, d, dtype=torch.bfloat16, device=dev)
+    t_tr2 = timed(lambda: et.expert_weight_transpose(w2, plan, out=w2t))
+    t_down_bwd = timed(lambda: et.expert_gemm_input_grad(dy, w2, plan, gather=True, row_scale=plan.slot_gate,
+                                                          wt=w2t, out=dh))
+    t_up_bwd = timed(lambda: et.expert_gemm_input_grad(dgu, w1, plan, wt=w1t, out=dxp))
+    dw1 = torch.empty(E, 2 * F, d, dtype=torch.float32, device=dev)
+    t_wg_up = timed(lambda: et.expert_gemm_weight_grad(dgu, xp, plan, out=dw1))
+    del dw1
+    dyp = torch.randn(S, d, device=dev, generator=g).to(torch.bfloat16)
+    dw2 = torch.empty(E, d, F, dtype=torch.float32, device=dev)
+    t_wg_down = timed(lambda: et.expert_gemm_weight_grad(dyp, a2, plan, out=dw2))
+    del dw2
+    try:      # torch's grouped GEMM in its weight-gradient form (sum over each group's rows)
+        t_wg_up_lib = timed(lambda: torch._grouped_mm(dgu.t(), xp, offs=offs))
+    except RuntimeError:
+        t_wg_up_lib = None
+    fl_wg_up = 2.0 * S * 2 * F * d
+    del w1, w2, h, a2, y, xp, dy, dgu, w2t, w1t, dh, dxp, dyp
     return {"kernel": "expert_gemm_kernel", "expert_ffn": F,
             "gate_up": {"K": d, "N": 2 * F, "mode": "gather (dispatch fused)", "ms": round(t_up, 3),
                         "TFLOP/s": round(fl_up / (t_up * 1e-3) / 1e12, 1),
@@ -280,7 +308,15 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
             "down": {"K": F, "N": d, "mode": "slot-major", "ms": round(t_down, 3),
                      "TFLOP/s": round(fl_down / (t_down * 1e-3) / 1e12, 1),
                      "frac": round(fl_down / (t_down * 1e-3) / MFMA_BF16_PEAK, 4),
-                     "torch_grouped_mm_ms": round(t_down_lib, 3)}}
+                     "torch_grouped_mm_ms": round(t_down_lib, 3)},
+            "backward": {"weight_transpose_down_ms": round(t_tr2, 3),
+                         "down_input_grad_fused_combine_bwd_ms": round(t_down_bwd, 3),
+                         "gate_up_input_grad_ms": round(t_up_bwd, 3),
+                         "gate_up_weight_grad_ms": round(t_wg_up, 3),
+                         "gate_up_weight_grad_TFLOP/s": round(fl_wg_up / (t_wg_up * 1e-3) / 1e12, 1),
+                         "down_weight_grad_ms": round(t_wg_down, 3),
+                         "torch_grouped_mm_gate_up_weight_grad_ms": (round(t_wg_up_lib, 3) if t_wg_up_lib
+                                                                     else None)}}
 
 
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
@@ -465,6 +501,11 @@ def main() -> int:
               f"epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} ms + dispatch "
               f"{gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; torch grouped "
               f"{dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
+        bw = eg["backward"]
+        print(f"  expert GEMM backward: down dA fused with the combine backward {bw['down_input_grad_fused_combine_bwd_ms']:.3f}"
+              f" ms (transpose {bw['weight_transpose_down_ms']:.3f}), gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, "
+              f"dW gate/up {bw['gate_up_weight_grad_ms']:.3f} ms (torch grouped {bw['torch_grouped_mm_gate_up_weight_grad_ms']}"
+              f"), dW down {bw['down_weight_grad_ms']:.3f} ms", file=sys.stderr)
 
     cpu = None
     if args.cpu_tokens > 0:

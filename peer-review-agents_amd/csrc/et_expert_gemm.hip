@@ -364,13 +364,22 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+        // The accumulators stay in the accumulation registers up to here (the
+        // epilogues' arithmetic would otherwise lead the register allocator to
+        // keep some in the vector registers the K loop needs).
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
         if constexpr (EPI == EPI_SWIGLU) {
             // h = (g * sigmoid(g)) * u in binary32, from the gate tiles j = 0, 1
             // and the up tiles j + 2 of the same lane and register; 128 hidden
             // columns per tile, wave column half wn holds hidden wn * 64 ...
-            // (one slot tile at a time keeps the sigmoid temporaries few)
-#pragma unroll 1
+            // (one slot tile at a time keeps the sigmoid temporaries few; the
+            // loop stays unrolled so that the accumulators are indexed statically)
+#pragma unroll
             for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
                 unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitchHalf;
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
@@ -643,24 +652,51 @@ __device__ __forceinline__ uint2 read_tr16(const unsigned char* p)
 __global__ __launch_bounds__(kThreads) void expert_wgrad_kernel(WgradArgs g)
 {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kStage];
+    __shared__ int ecnt[ET_MAX_EXPERTS];           // slots per expert
+    __shared__ int order[ET_MAX_EXPERTS];          // experts by decreasing slot count
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int E = g.E, K = g.K, N = g.N;
     const int wm = wave >> 1, wn = wave & 1;
     const int nNt = (N + kBN - 1) / kBN, nKt = (K + kBN - 1) / kBN;
-    const int Q = E * nNt * nKt;
+    const int tpe = nNt * nKt;                     // tiles per expert
+    const int Q = E * tpe;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
+
+    // Work balance with locality.  A tile reduces over all of its expert's
+    // slots, so tiles of heavily routed experts cost up to thousands of times
+    // more than the others.  Experts are ordered by decreasing slot count
+    // (ties by index) and the tiles dealt out round-robin in that order:
+    // every block gets the same number of heavy tiles (within one), and the
+    // blocks running together work on tiles of the same expert, which share
+    // its operand rows through L2.
+    for (int e = threadIdx.x; e < E; e += kThreads) {
+        const int64_t lo = min<int64_t>(g.expert_offsets[e], g.cap);
+        const int64_t hi = min<int64_t>(g.expert_offsets[e + 1], g.cap);
+        ecnt[e] = (int)max<int64_t>(0, hi - lo);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += kThreads) {
+        const int ce = ecnt[e];
+        int rank = 0;
+        for (int f = 0; f < E; ++f) {
+            const int cf = ecnt[f];
+            rank += (cf > ce || (cf == ce && f < e)) ? 1 : 0;
+        }
+        order[rank] = e;
+    }
+    __syncthreads();
 
     // Direct loads of a chunk: wave w fills row pairs 8 w + i (i < 8) of each
     // operand, rows r = 16 w + 2 i + lane / 32, 16-byte slot q = lane % 32,
     // holding column segment q ^ (4 (r & 3)).
     // Fragment reads (tile t of 32 columns, k-step ks of 16 slots, half h):
     // lane l reads row 16 ks + 8 (l / 32) + 4 h + j / 4 (j = l % 16), columns
-    // 32 t + 16 ((l / 16) % 2) + 4 (j % 4) .. + 3.
-    // Per-lane LDS offset of tile t's fragment at k-step 0, half 0; k-step ks
-    // and half h add (16 ks + 4 h) * 512 bytes (the row & 3 of the swizzle is
-    // j / 4 for every ks and h).
+    // 32 t + 16 ((l / 16) % 2) + 4 (j % 4) .. + 3.  Per-lane LDS offset of
+    // tile t's fragment at k-step 0, half 0; k-step ks and half h add
+    // (16 ks + 4 h) * 512 bytes (the row & 3 of the swizzle is j / 4 for
+    // every ks and h).
     const int jj = lane & 15;
     uint32_t fb[2][4];
 #pragma unroll
@@ -673,10 +709,9 @@ __global__ __launch_bounds__(kThreads) void expert_wgrad_kernel(WgradArgs g)
             fb[o][t] = (uint32_t)((8 * (lane >> 5) + (jj >> 2)) * 512 + slot * 16 + (jj & 1) * 8 + o * kHalf);
         }
     }
-
     for (int q = blockIdx.x; q < Q; q += gridDim.x) {
-        const int e = q / (nNt * nKt);
-        const int rem = q - e * nNt * nKt;
+        const int e = order[q / tpe];
+        const int rem = q % tpe;
         const int n0 = (rem / nKt) * kBN, k0 = (rem % nKt) * kBN;
         const int64_t lo = min<int64_t>(g.expert_offsets[e], g.cap);
         const int64_t hi = min<int64_t>(g.expert_offsets[e + 1], g.cap);
