@@ -163,3 +163,75 @@ def test_manual_bf16_training_step_with_router_kernels(dev):
     close(y, yr, "y", 2e-2)
     close(dx, xr.grad, "dX", 3e-2)
     close(dwr, wr.grad, "dW_router", 3e-2)
+
+
+def test_bf16_moe_layer_entirely_on_library_kernels(dev):
+    """A bf16 SwiGLU-expert MoE layer with every GEMM and data movement on this
+    library's kernels, the way a fused training step would run it:
+      forward:  router_logits -> route -> expert_gemm(X, W1) gathered (the
+                dispatch fused) -> SwiGLU -> expert_gemm(., W2) -> combine;
+      backward: combine_backward (dgate, dlogits, dYp) ->
+                expert_gemm_input_grad(dY, W2) gathered, rows times the slot
+                gate (the down projection's input gradient fused with the
+                combine backward) -> SwiGLU backward (torch elementwise) ->
+                expert_gemm_input_grad(dGU, W1) -> dispatch_backward with the
+                router's input gradient; expert_gemm_weight_grad for W1 and W2
+                (the gathered operand dispatched once), router_weight_grad.
+    Output and every gradient against a float64 restatement with the same
+    routed pairs, at the bf16 bar (several bf16 roundings on the path)."""
+    et = importlib.import_module("peer-review-agents_amd")
+    T, d, E, F = 1024, 256, 16, 128
+    g = torch.Generator().manual_seed(11)
+    bf = torch.bfloat16
+    X = torch.randn(T, d, generator=g).to(bf).to(dev)
+    Wr = (torch.randn(E, d, generator=g) * d ** -0.5).to(bf).to(dev)
+    W1 = (torch.randn(E, 2 * F, d, generator=g) * d ** -0.5).to(bf).to(dev)     # gate rows, then up rows
+    W2 = (torch.randn(E, d, F, generator=g) * F ** -0.5).to(bf).to(dev)
+    dy = (torch.randn(T, d, generator=g) * 0.1).to(bf).to(dev)
+
+    logits = et.router_logits(X, Wr)
+    thr = torch.quantile(torch.sigmoid(logits.double()), 0.8, dim=0).float().contiguous()
+    plan = et.route(logits, thr)
+    gu = et.expert_gemm(X, W1, plan)                       # [S, 2F] pre-activations
+    hact = et.expert_gemm(X, W1, plan, epilogue="swiglu")   # [S, F], fused activation
+    yp = et.expert_gemm(hact, W2, plan, gather=False)
+    y = et.combine(yp, plan)
+
+    dyp, dgate, dlogits = et.combine_backward(dy, yp, plan, need_dlogits=True)
+    dh = et.expert_gemm_input_grad(dy, W2, plan, gather=True, row_scale=plan.slot_gate)
+    gf, uf = gu[:, :F].float(), gu[:, F:].float()
+    sg = torch.sigmoid(gf)
+    dhf = dh.float()
+    dgate_pre = dhf * uf * sg * (1 + gf * (1 - sg))
+    dup = dhf * gf * sg
+    dgu = torch.cat([dgate_pre, dup], 1).to(bf).contiguous()
+    dxp = et.expert_gemm_input_grad(dgu, W1, plan)
+    dx = et.dispatch_backward(dxp, plan, router_weight=Wr, dgate=dgate)
+    dW1 = et.expert_gemm_weight_grad(dgu, et.dispatch(X, plan), plan)
+    dW2 = et.expert_gemm_weight_grad(dyp, hact, plan)
+    dWr = et.router_weight_grad(dlogits, X)
+
+    st = plan.sorted_token.long().cpu()
+    ee = torch.repeat_interleave(torch.arange(E), plan.counts.long().cpu())
+    xr = X.cpu().double().requires_grad_(True)
+    wr = Wr.cpu().double().requires_grad_(True)
+    w1 = W1.cpu().double().requires_grad_(True)
+    w2 = W2.cpu().double().requires_grad_(True)
+    gate = torch.sigmoid((xr @ wr.T)[st, ee])
+    pre = torch.bmm(w1[ee], xr[st].unsqueeze(2)).squeeze(2)                  # [S, 2F]
+    act = torch.nn.functional.silu(pre[:, :F]) * pre[:, F:]
+    ys = torch.bmm(w2[ee], act.unsqueeze(2)).squeeze(2)                     # [S, d]
+    yr = torch.zeros(T, d, dtype=torch.float64).index_add(0, st, gate[:, None] * ys)
+    yr.backward(dy.cpu().double())
+
+    def close(a, b, name, rel):
+        a = a.detach().cpu().double()
+        scale = b.abs().max().item() + 1e-12
+        err = (a - b.detach()).abs().max().item()
+        assert err <= rel * scale, f"{name}: max error {err:.3e} vs scale {scale:.3e}"
+
+    close(y, yr, "y", 2e-2)
+    close(dx, xr.grad, "dX", 3e-2)
+    close(dW1, w1.grad, "dW1", 3e-2)
+    close(dW2, w2.grad, "dW2", 3e-2)
+    close(dWr, wr.grad, "dW_router", 3e-2)
