@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 5
+#define ET_ABI_VERSION 6
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -310,6 +310,30 @@ int et_expert_weight_transpose(const void* w, const int32_t* expert_offsets, int
  */
 int et_expert_wgrad(const void* dc, const void* a, const int32_t* expert_offsets, int64_t num_experts,
                     int64_t N, int64_t K, int64_t slot_capacity, float* dw, void* stream);
+
+/*
+ * SwiGLU of the expert FFN, element-wise over the routed slots
+ * s < min(expert_offsets[E], slot_capacity), j < F:
+ *   et_swiglu_fwd:  h[s, j] = (g * sigmoid(g)) * u
+ *   et_swiglu_bwd:  dgu[s, j]     = (dh * u) * (sigmoid(g) * (1 + g * (1 - sigmoid(g))))
+ *                   dgu[s, F + j] = dh * (g * sigmoid(g))
+ * with g = gu[s, j], u = gu[s, F + j], dh = dh[s, j].  gu bf16 [slot_capacity,
+ * 2F] is the gate/up projection's output (et_expert_gemm without epilogue:
+ * gate rows of the weight first), h and dh bf16 [slot_capacity, F], dgu bf16
+ * [slot_capacity, 2F].  Binary32 arithmetic, each operation rounded in the
+ * order written (no fused multiply-add), the routing's sigmoid; one rounding
+ * to bf16 per output.  The forward gives the same bits as the
+ * ET_GEMM_SWIGLU epilogue applied to the rounded gu (the epilogue itself works
+ * on the unrounded accumulators).  Rows past the routed slots are left as they
+ * were; the slot count is read on the device (no host synchronisation).  F a
+ * multiple of 8; every pointer 16-byte aligned.  Implements the expert FFN's
+ * activation for training, where gu is kept for the backward (no reference
+ * counterpart).
+ */
+int et_swiglu_fwd(const void* gu, int64_t F, const int32_t* expert_offsets, int64_t num_experts,
+                  int64_t slot_capacity, void* h, void* stream);
+int et_swiglu_bwd(const void* gu, const void* dh, int64_t F, const int32_t* expert_offsets,
+                  int64_t num_experts, int64_t slot_capacity, void* dgu, void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,10 @@ _p = ctypes.c_void_p
 
 def build(force: bool = False) -> str:
     """Compile the C restatement with the committed Makefile."""
-    if force or not os.path.exists(_LIB_PATH):
+    src = os.path.join(_HERE, "etmoe_oracle.c")
+    stale = not os.path.exists(_LIB_PATH) or (
+        os.path.exists(src) and os.path.getmtime(src) > os.path.getmtime(_LIB_PATH))
+    if force or stale:
         subprocess.run(["make", "-s", "-C", _HERE] + (["-B"] if force else []),
                        check=True)
     return _LIB_PATH
@@ -57,6 +60,14 @@ def lib() -> ctypes.CDLL:
         L.oracle_sigmoid.argtypes = [ctypes.c_float]
         L.oracle_swiglu.restype = ctypes.c_float
         L.oracle_swiglu.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.oracle_swiglu_grad_f32.restype = None
+        L.oracle_swiglu_grad_f32.argtypes = [_p, _p, _p, _i64, _p, _p]
+        L.oracle_swiglu_f32.restype = None
+        L.oracle_swiglu_f32.argtypes = [_p, _p, _i64, _p]
+        L.oracle_swiglu_fwd_rows.restype = None
+        L.oracle_swiglu_fwd_rows.argtypes = [_p, _i64, _i64, _p]
+        L.oracle_swiglu_bwd_rows.restype = None
+        L.oracle_swiglu_bwd_rows.argtypes = [_p, _p, _i64, _i64, _p]
         L.oracle_sigmoid_order_scan.restype = None
         L.oracle_sigmoid_order_scan.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _p]
         L.oracle_select.restype = _i64
@@ -136,13 +147,41 @@ def sigmoid(logits: np.ndarray) -> np.ndarray:
 
 def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     """Element-wise (g * sigmoid(g)) * u in binary32 (oracle_swiglu; tests only)."""
-    L = lib()
     gf = _c(g, np.float32).ravel()
     uf = _c(u, np.float32).ravel()
     out = np.empty_like(gf)
-    for i in range(gf.size):
-        out[i] = L.oracle_swiglu(float(gf[i]), float(uf[i]))
+    lib().oracle_swiglu_f32(_ptr(gf), _ptr(uf), gf.size, _ptr(out))
     return out.reshape(np.shape(g))
+
+
+def swiglu_grad(g: np.ndarray, u: np.ndarray, dh: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(dg, du) of h = (g * sigmoid(g)) * u for upstream dh, binary32
+    (oracle_swiglu_grad; tests only)."""
+    gf, uf, df = (_c(x, np.float32).ravel() for x in (g, u, dh))
+    dg, du = np.empty_like(gf), np.empty_like(gf)
+    lib().oracle_swiglu_grad_f32(_ptr(gf), _ptr(uf), _ptr(df), gf.size, _ptr(dg), _ptr(du))
+    return dg.reshape(np.shape(g)), du.reshape(np.shape(g))
+
+
+def swiglu_rows(gu_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits [n, F] of h from bf16 bits gu [n, 2F] (oracle_swiglu_fwd_rows)."""
+    gu = _c(gu_bits, np.uint16)
+    n, F2 = gu.shape
+    h = np.empty((n, F2 // 2), dtype=np.uint16)
+    lib().oracle_swiglu_fwd_rows(_ptr(gu), n, F2 // 2, _ptr(h))
+    return h
+
+
+def swiglu_backward_rows(gu_bits: np.ndarray, dh_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits [n, 2F] of (dg | du) from bf16 bits gu [n, 2F] and dh [n, F]
+    (oracle_swiglu_bwd_rows)."""
+    gu = _c(gu_bits, np.uint16)
+    dh = _c(dh_bits, np.uint16)
+    n, F2 = gu.shape
+    assert dh.shape == (n, F2 // 2)
+    out = np.empty_like(gu)
+    lib().oracle_swiglu_bwd_rows(_ptr(gu), _ptr(dh), n, F2 // 2, _ptr(out))
+    return out
 
 
 def exp_nonpos(x: np.ndarray) -> np.ndarray:

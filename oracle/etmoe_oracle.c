@@ -123,6 +123,61 @@ float oracle_swiglu(float g, float u)
     return gs * u;
 }
 
+/* Gradients of h = (g * sigmoid(g)) * u for an upstream dh, in binary32 with
+ * every operation rounded in the order written:
+ *   dg = (dh * u) * (s * (1 + g * (1 - s))),   du = dh * (g * s),   s = sigmoid(g)
+ * (d/dg of g * s is s + g s (1 - s)).  Infinite g gives NaN in dg (0 * inf).
+ * Pinned in tests/test_oracle.py against float64 derivatives of the float64
+ * forward (analytic and central differences) and exact special values. */
+void oracle_swiglu_grad(float g, float u, float dh, float* dg, float* du)
+{
+    const float s = oracle_sigmoid(g);
+    const float t = 1.0f - s;
+    const float q = g * t;
+    const float r = 1.0f + q;
+    const float v = s * r;
+    const float w = dh * u;
+    *dg = w * v;
+    const float gs = g * s;
+    *du = dh * gs;
+}
+
+/* Element-wise forms over float arrays (for the pinning tests). */
+void oracle_swiglu_grad_f32(const float* g, const float* u, const float* dh, int64_t n, float* dg, float* du)
+{
+    for (int64_t i = 0; i < n; ++i) oracle_swiglu_grad(g[i], u[i], dh[i], &dg[i], &du[i]);
+}
+
+void oracle_swiglu_f32(const float* g, const float* u, int64_t n, float* h)
+{
+    for (int64_t i = 0; i < n; ++i) h[i] = oracle_swiglu(g[i], u[i]);
+}
+
+/* Slot-row forms on bf16 buffers, as et_swiglu_fwd / et_swiglu_bwd lay them
+ * out: gu [n, 2F] (gate columns first, then up), h and dh [n, F], dgu [n, 2F]
+ * (dg columns first); each output rounded once to bf16 (nearest even). */
+void oracle_swiglu_fwd_rows(const uint16_t* gu, int64_t n, int64_t F, uint16_t* h)
+{
+    for (int64_t s = 0; s < n; ++s)
+        for (int64_t j = 0; j < F; ++j) {
+            const float g = oracle_bf16_to_f32(gu[s * 2 * F + j]);
+            const float u = oracle_bf16_to_f32(gu[s * 2 * F + F + j]);
+            h[s * F + j] = oracle_f32_to_bf16(oracle_swiglu(g, u));
+        }
+}
+
+void oracle_swiglu_bwd_rows(const uint16_t* gu, const uint16_t* dh, int64_t n, int64_t F, uint16_t* dgu)
+{
+    for (int64_t s = 0; s < n; ++s)
+        for (int64_t j = 0; j < F; ++j) {
+            float dg, du;
+            oracle_swiglu_grad(oracle_bf16_to_f32(gu[s * 2 * F + j]), oracle_bf16_to_f32(gu[s * 2 * F + F + j]),
+                               oracle_bf16_to_f32(dh[s * F + j]), &dg, &du);
+            dgu[s * 2 * F + j] = oracle_f32_to_bf16(dg);
+            dgu[s * 2 * F + F + j] = oracle_f32_to_bf16(du);
+        }
+}
+
 /* Order scan of the sigmoid: over the floats with order index k in [k0, k1)
  * (k < 2^31: the negative floats from the most negative up to -0, as bit
  * patterns 0xFFFFFFFF - k; k >= 2^31: +0 up to +inf, bit patterns k - 2^31),

@@ -25,6 +25,8 @@ from .expert_threshold import (  # noqa: F401
     router_route,
     router_route_workspace_bytes,
     router_weight_grad,
+    swiglu,
+    swiglu_backward,
     threshold_update_,
     threshold_workspace_bytes,
 )

@@ -63,6 +63,8 @@ _SIGNATURES = {
     "et_expert_gemm": (_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _p, _p]),
     "et_expert_weight_transpose": (_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "et_expert_wgrad": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "et_swiglu_fwd": (_int, [_p, _i64, _p, _i64, _i64, _p, _p]),
+    "et_swiglu_bwd": (_int, [_p, _p, _i64, _p, _i64, _i64, _p, _p]),
 }
 
 _lib = None

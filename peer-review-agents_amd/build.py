@@ -13,7 +13,7 @@ import sys
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_HERE)
 SOURCES = ["et_abi.hip", "et_route.hip", "et_rows.hip", "et_threshold.hip", "et_router.hip", "et_router_bwd.hip",
-           "et_expert_gemm.hip"]
+           "et_expert_gemm.hip", "et_swiglu.hip"]
 OUT = os.path.join(_HERE, "libetmoe.so")
 ARCH = os.environ.get("ET_OFFLOAD_ARCH", "gfx950")
 

@@ -475,6 +475,54 @@ def expert_gemm_weight_grad(dc: torch.Tensor, a: torch.Tensor, plan: RoutingPlan
     return dw
 
 
+def _swiglu_args(gu: torch.Tensor, plan: RoutingPlan) -> int:
+    _require(gu, "gu", torch.bfloat16, 2)
+    _check_plan(plan, gu.device)
+    if gu.shape[0] != plan.rows:
+        raise ValueError(f"gu must have {plan.rows} rows (the plan's slot capacity)")
+    if gu.shape[1] % 16:
+        raise ValueError("gu must have 2F columns with F a multiple of 8")
+    return gu.shape[1] // 2
+
+
+def swiglu(gu: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """SwiGLU of the expert FFN for training: h[s, j] = silu(g) * u with g =
+    gu[s, j], u = gu[s, F + j] (gu = expert_gemm(...) without epilogue, kept for
+    :func:`swiglu_backward`), bf16 [rows, F].  Same bits as the GEMM's
+    ``epilogue="swiglu"`` applied to the rounded gu.  Rows past the routed slots
+    are left as they were."""
+    F = _swiglu_args(gu, plan)
+    dev = gu.device
+    h = _out_or_new(out, (plan.rows, F), torch.bfloat16, dev, "out")
+    if gu.data_ptr() % 16 or h.data_ptr() % 16:
+        raise ValueError("gu and out must be 16-byte aligned")
+    with torch.cuda.device(dev):
+        rc = lib().et_swiglu_fwd(_vp(gu), F, _vp(plan.expert_offsets), plan.num_experts, plan.rows, _vp(h),
+                                 _stream(dev))
+    check("et_swiglu_fwd", rc)
+    return h
+
+
+def swiglu_backward(gu: torch.Tensor, dh: torch.Tensor, plan: RoutingPlan,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Backward of :func:`swiglu`: dgu = [dh * u * silu'(g) | dh * silu(g)],
+    bf16 [rows, 2F] (the gate/up projection's output gradient, ready for
+    :func:`expert_gemm_input_grad` and :func:`expert_gemm_weight_grad`)."""
+    F = _swiglu_args(gu, plan)
+    dev = gu.device
+    _require(dh, "dh", torch.bfloat16, 2, dev)
+    if tuple(dh.shape) != (plan.rows, F):
+        raise ValueError(f"dh must be [{plan.rows}, {F}]")
+    dgu = _out_or_new(out, (plan.rows, 2 * F), torch.bfloat16, dev, "out")
+    if gu.data_ptr() % 16 or dh.data_ptr() % 16 or dgu.data_ptr() % 16:
+        raise ValueError("gu, dh and out must be 16-byte aligned")
+    with torch.cuda.device(dev):
+        rc = lib().et_swiglu_bwd(_vp(gu), _vp(dh), F, _vp(plan.expert_offsets), plan.num_experts, plan.rows,
+                                 _vp(dgu), _stream(dev))
+    check("et_swiglu_bwd", rc)
+    return dgu
+
+
 # --------------------------------------------------------------------------- #
 # EMA threshold update
 # --------------------------------------------------------------------------- #

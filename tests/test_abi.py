@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 21
+    assert len(syms) == 23
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name
@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 5" in hdr
-    assert et.lib().et_abi_version() == 5
+    assert "#define ET_ABI_VERSION 6" in hdr
+    assert et.lib().et_abi_version() == 6
 
 
 def test_workspace_sizes(et):
@@ -161,3 +161,26 @@ def test_expert_gemm_rejects_bad_arguments(et):
         == ET_ERR_INVALID_ARGUMENT
     # no slot rows: nothing to do, nothing launched
     assert lib.et_expert_gemm(p, 16, p, p, p, 4, 64, 64, 0, 0, None, p, None) == 0
+
+
+def test_swiglu_rejects_bad_arguments(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    # et_swiglu_fwd(gu, F, expert_offsets, E, slot_capacity, h, stream)
+    assert lib.et_swiglu_fwd(p, 12, p, 4, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "multiple of 8" in _err(et)
+    assert lib.et_swiglu_fwd(p, 16, p, 0, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "num_experts" in _err(et)
+    assert lib.et_swiglu_fwd(p, 16, p, 4, -1, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_swiglu_fwd(p, 16, None, 4, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "null" in _err(et)
+    assert lib.et_swiglu_fwd(ctypes.c_void_p(0x1008), 16, p, 4, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "aligned" in _err(et)
+    # et_swiglu_bwd(gu, dh, F, expert_offsets, E, slot_capacity, dgu, stream)
+    assert lib.et_swiglu_bwd(p, None, 16, p, 4, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "null" in _err(et)
+    assert lib.et_swiglu_bwd(p, ctypes.c_void_p(0x1004), 16, p, 4, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_swiglu_bwd(p, p, 0, p, 4, 16, p, None) == ET_ERR_INVALID_ARGUMENT
+    # no slot rows: nothing to do, nothing launched
+    assert lib.et_swiglu_fwd(p, 16, p, 4, 0, p, None) == 0
+    assert lib.et_swiglu_bwd(p, p, 16, p, 4, 0, p, None) == 0

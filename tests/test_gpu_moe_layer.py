@@ -173,7 +173,7 @@ def test_bf16_moe_layer_entirely_on_library_kernels(dev):
       backward: combine_backward (dgate, dlogits, dYp) ->
                 expert_gemm_input_grad(dY, W2) gathered, rows times the slot
                 gate (the down projection's input gradient fused with the
-                combine backward) -> SwiGLU backward (torch elementwise) ->
+                combine backward) -> swiglu_backward on the kept gu ->
                 expert_gemm_input_grad(dGU, W1) -> dispatch_backward with the
                 router's input gradient; expert_gemm_weight_grad for W1 and W2
                 (the gathered operand dispatched once), router_weight_grad.
@@ -199,12 +199,11 @@ def test_bf16_moe_layer_entirely_on_library_kernels(dev):
 
     dyp, dgate, dlogits = et.combine_backward(dy, yp, plan, need_dlogits=True)
     dh = et.expert_gemm_input_grad(dy, W2, plan, gather=True, row_scale=plan.slot_gate)
-    gf, uf = gu[:, :F].float(), gu[:, F:].float()
-    sg = torch.sigmoid(gf)
-    dhf = dh.float()
-    dgate_pre = dhf * uf * sg * (1 + gf * (1 - sg))
-    dup = dhf * gf * sg
-    dgu = torch.cat([dgate_pre, dup], 1).to(bf).contiguous()
+    dgu = et.swiglu_backward(gu, dh, plan)
+    # the training forward's activation (from the kept, rounded gu) is within
+    # one bf16 rounding of the fused epilogue's (from the binary32 accumulators)
+    htrain = et.swiglu(gu, plan).float()
+    assert (htrain - hact.float()).abs().max().item() <= 2 ** -7 * hact.float().abs().max().item()
     dxp = et.expert_gemm_input_grad(dgu, W1, plan)
     dx = et.dispatch_backward(dxp, plan, router_weight=Wr, dgate=dgate)
     dW1 = et.expert_gemm_weight_grad(dgu, et.dispatch(X, plan), plan)

@@ -88,6 +88,61 @@ def test_swiglu_within_a_few_ulp_of_float64(orc):
     assert not np.array_equal(orc.swiglu(u, g), got)
 
 
+def test_swiglu_grad_matches_float64_derivatives(orc):
+    """oracle_swiglu_grad against float64 derivatives of the float64 forward
+    silu(g) * u, each by a route that does not share the oracle's expression:
+    du against d/du = silu(g) (relative, a few ulp); dg against the analytic
+    d/dg = u * (s + g s (1 - s)) and against central differences of the
+    forward, within the rounding bound 16 eps |dh u| s (1 + |g|) (the
+    propagated error of the binary32 evaluation; a dropped "1 +", a swapped
+    s / 1 - s or a transposed g, u misses it by orders of magnitude)."""
+    rng = np.random.default_rng(11)
+    g = np.concatenate([np.linspace(-30.0, 30.0, 6001), rng.standard_normal(4000) * 3]).astype(np.float32)
+    u = (rng.standard_normal(g.size) * 2).astype(np.float32)
+    dh = rng.standard_normal(g.size).astype(np.float32)
+    dg, du = orc.swiglu_grad(g, u, dh)
+    g64, u64, d64 = (x.astype(np.float64) for x in (g, u, dh))
+    s64 = 1.0 / (1.0 + np.exp(-g64))
+    eps = 2.0 ** -24
+    bound = 16 * eps * np.abs(d64 * u64) * s64 * (1 + np.abs(g64)) + 1e-37
+    analytic = d64 * u64 * (s64 + g64 * s64 * (1 - s64))
+    assert np.all(np.abs(dg - analytic) <= bound)
+    f = lambda x: x / (1.0 + np.exp(-x)) * u64                  # noqa: E731  float64 forward
+    delta = 1e-5
+    fd = d64 * (f(g64 + delta) - f(g64 - delta)) / (2 * delta)
+    assert np.all(np.abs(dg - fd) <= bound + 1e-8 * np.abs(d64 * u64))
+    du_ref = (d64 * g64 * s64).astype(np.float32)
+    big = np.abs(du_ref) > 1e-30
+    assert ulp_diff(du[big], du_ref[big]).max() <= 6
+    # du is dh times the forward at u = 1, bit for bit (same binary32 steps)
+    assert np.array_equal(du, dh * orc.swiglu(g, np.ones_like(g)))
+    # exact special values: s(0) = 1/2; s(50) = 1 in binary32
+    dg0, du0 = orc.swiglu_grad(np.float32([0.0, 50.0]), np.float32([3.0, 3.0]), np.float32([0.5, 0.5]))
+    assert dg0.tolist() == [0.75, 1.5] and du0.tolist() == [0.0, 25.0]
+    dgi, _ = orc.swiglu_grad(np.float32([-np.inf]), np.float32([1.0]), np.float32([1.0]))
+    assert np.isnan(dgi[0])                                     # 0 * inf, as documented
+
+
+def test_swiglu_row_forms_lay_out_gate_then_up(orc):
+    """The bf16 slot-row forms: gu row = [g_0..g_{F-1}, u_0..u_{F-1}], h[s, j]
+    = bf16(swiglu(g, u)), dgu row = [dg..., du...]; the bf16 rounding checked
+    against torch's round-to-nearest-even."""
+    rng = np.random.default_rng(5)
+    n, F = 37, 24
+    gu = torch.from_numpy(rng.standard_normal((n, 2 * F)).astype(np.float32) * 3).to(torch.bfloat16)
+    dh = torch.from_numpy(rng.standard_normal((n, F)).astype(np.float32)).to(torch.bfloat16)
+    gu_bits = gu.view(torch.int16).numpy().view(np.uint16)
+    dh_bits = dh.view(torch.int16).numpy().view(np.uint16)
+    g, u = gu[:, :F].float().numpy(), gu[:, F:].float().numpy()
+    h = orc.swiglu_rows(gu_bits)
+    want = torch.from_numpy(orc.swiglu(g, u)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(h, want)
+    dgu = orc.swiglu_backward_rows(gu_bits, dh_bits)
+    dg, du = orc.swiglu_grad(g, u, dh.float().numpy())
+    to16 = lambda x: torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    assert np.array_equal(dgu[:, :F], to16(dg)) and np.array_equal(dgu[:, F:], to16(du))
+
+
 def test_sigmoid_is_monotone_up_to_two_order_steps_over_all_floats(orc):
     """Exhaustive over all 2^32 bit patterns (NaN logits skipped): the
     specified sigmoid never returns a negative score, and each score is at most
