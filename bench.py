@@ -253,7 +253,8 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     needs the dispatched Xp, so the dispatch is timed beside it.  The gate/up
     projection is also timed with the SwiGLU epilogue (half the output), and
     the backward of both projections: the input gradients (the down one fused
-    with the combine backward) and the f32 weight gradients.  Random-init
+    with the combine backward) and the f32 weight gradients, and the
+    element-wise SwiGLU for training (forward and backward).  Random-init
     expert weights of that shape; measured after the timed step with HIP events
     on the stream the kernels run on."""
     import torch
@@ -304,6 +305,15 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     t_down_bwd = timed(lambda: et.expert_gemm_input_grad(dy, w2, plan, gather=True, row_scale=plan.slot_gate,
                                                           wt=w2t, out=dh))
     t_up_bwd = timed(lambda: et.expert_gemm_input_grad(dgu, w1, plan, wt=w1t, out=dxp))
+    # the activation for training, on the kept gate/up output h (HBM-bound:
+    # 6F bytes per slot forward, 10F backward)
+    hs = torch.empty(S, F, dtype=torch.bfloat16, device=dev)
+    dgu2 = torch.empty(S, 2 * F, dtype=torch.bfloat16, device=dev)
+    t_sw = timed(lambda: et.swiglu(h, plan, out=hs))
+    t_sw_bwd = timed(lambda: et.swiglu_backward(h, dh, plan, out=dgu2))
+    del hs, dgu2
+    sw_gbs = 6.0 * F * S / (t_sw * 1e-3) / 1e9
+    sw_bwd_gbs = 10.0 * F * S / (t_sw_bwd * 1e-3) / 1e9
     dw1 = torch.empty(E, 2 * F, d, dtype=torch.float32, device=dev)
     t_wg_up = timed(lambda: et.expert_gemm_weight_grad(dgu, xp, plan, out=dw1))
     del dw1
@@ -335,7 +345,11 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
                          "gate_up_weight_grad_TFLOP/s": round(fl_wg_up / (t_wg_up * 1e-3) / 1e12, 1),
                          "down_weight_grad_ms": round(t_wg_down, 3),
                          "torch_grouped_mm_gate_up_weight_grad_ms": (round(t_wg_up_lib, 3) if t_wg_up_lib
-                                                                     else None)}}
+                                                                     else None)},
+            "swiglu": {"forward_ms": round(t_sw, 3), "forward_GB/s": round(sw_gbs, 1),
+                       "forward_frac": round(sw_gbs * 1e9 / HBM_PEAK, 4), "backward_ms": round(t_sw_bwd, 3),
+                       "backward_GB/s": round(sw_bwd_gbs, 1),
+                       "backward_frac": round(sw_bwd_gbs * 1e9 / HBM_PEAK, 4)}}
 
 
 def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
@@ -547,6 +561,9 @@ def main() -> int:
               f" ms (transpose {bw['weight_transpose_down_ms']:.3f}), gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, "
               f"dW gate/up {bw['gate_up_weight_grad_ms']:.3f} ms (torch grouped {bw['torch_grouped_mm_gate_up_weight_grad_ms']}"
               f"), dW down {bw['down_weight_grad_ms']:.3f} ms", file=sys.stderr)
+        sw = eg["swiglu"]
+        print(f"  SwiGLU for training: forward {sw['forward_ms']:.3f} ms ({100 * sw['forward_frac']:.1f}% of peak), "
+              f"backward {sw['backward_ms']:.3f} ms ({100 * sw['backward_frac']:.1f}% of peak)", file=sys.stderr)
 
     cpu = None
     if args.cpu_tokens > 0:
