@@ -124,3 +124,60 @@ def test_graph_replays_match_eager_router_kernels(et, dev):
             if i in (4, 5, 6):                          # slot arrays: the first S entries are defined
                 a, b = a[:S], b[:S]
             assert torch.equal(_bits(a), _bits(b)), (rep, i)
+
+
+def _ffn_path(et, x, w1, w2, dy, plan):
+    gu = et.expert_gemm(x, w1, plan)                                   # gathered gate/up
+    h = et.swiglu(gu, plan)
+    hf = et.expert_gemm(x, w1, plan, epilogue="swiglu")
+    yp = et.expert_gemm(h, w2, plan, gather=False)
+    y = et.combine(yp, plan)
+    dyp, dgate, _ = et.combine_backward(dy, yp, plan)
+    dh = et.expert_gemm_input_grad(dy, w2, plan, gather=True, row_scale=plan.slot_gate)
+    dgu = et.swiglu_backward(gu, dh, plan)
+    dxp = et.expert_gemm_input_grad(dgu, w1, plan)
+    dx = et.dispatch_backward(dxp, plan)
+    dw1 = et.expert_gemm_weight_grad(dgu, et.dispatch(x, plan), plan)
+    dw2 = et.expert_gemm_weight_grad(dyp, h, plan)
+    slot_rows = [gu, h, hf, yp, dyp, dgate, dh, dgu, dxp]
+    return slot_rows, [y, dx, dw1, dw2]
+
+
+def test_graph_replays_match_eager_expert_ffn(et, dev):
+    """A SwiGLU expert FFN on the library -- gathered gate/up GEMM, training
+    SwiGLU and the fused epilogue, down GEMM, combine, combine backward, the
+    fused down input gradient (with the weight transpose), SwiGLU backward,
+    gate/up input gradient, dispatch backward and both weight gradients --
+    captured in one HIP graph: every replay equals eager bit for bit."""
+    T, d, E, F = 1024, 256, 8, 128
+    g = torch.Generator(device=dev)
+    g.manual_seed(31)
+    logits = torch.randn(T, E, device=dev, generator=g)
+    thr = torch.full((E,), 0.7, device=dev)
+    S = et.route(logits, thr).num_slots
+    plan = et.route(logits, thr, slot_capacity=S + 48)
+    x = torch.randn(T, d, device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(E, 2 * F, d, device=dev, generator=g) * d ** -0.5).to(torch.bfloat16)
+    w2 = (torch.randn(E, d, F, device=dev, generator=g) * F ** -0.5).to(torch.bfloat16)
+    dy = (torch.randn(T, d, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+
+    rows_e, full_e = _ffn_path(et, x, w1, w2, dy, plan)
+    eager = [t[:S].clone() for t in rows_e] + [t.clone() for t in full_e]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        _ffn_path(et, x, w1, w2, dy, plan)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rows_g, full_g = _ffn_path(et, x, w1, w2, dy, plan)
+    for rep in range(3):
+        for t in rows_g + full_g:
+            t.zero_() if t.dtype != torch.bfloat16 else t.view(torch.int16).zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t[:S] for t in rows_g] + full_g
+        for i, (a, b) in enumerate(zip(got, eager)):
+            assert torch.equal(_bits(a), _bits(b)), (rep, i)
