@@ -24,8 +24,9 @@
 // bytes (64 k) per row, and the 16-byte segment s of row R sits at slot
 // s ^ key(R), key(R) = (R & 7) ^ ((R >> 3) & 1): the fragment reads (lane l:
 // row l % 32, segment 2 * kstep + l / 32) then hit 16 distinct slots of every
-// 256-byte bank window, with no bank conflicts.  The output tile goes back
-// through LDS so that it is stored in whole rows.
+// 256-byte bank window, with no bank conflicts.  The output goes straight
+// from the accumulators to memory (16 bytes per lane after a lane-pair swap),
+// leaving the stages to the next tile.
 //
 // MFMA 32x32x16 bf16 operand layout (checked on the device by the router
 // kernels): lane l holds A row l % 32 and B column l % 32 at k = 8 (l / 32) + i;
@@ -44,7 +45,10 @@
 // x is given the contiguous range of tiles [x * per, (x + 1) * per); inside an
 // expert, tiles are ordered in groups of 8 slot tiles x every feature tile, so
 // the ~32 blocks running together on one XCD share 8 A tiles and 4 W tiles
-// through that XCD's L2.
+// through that XCD's L2.  A block's tiles form one stream of chunks: the last
+// two chunks of a tile load the next tile's first two, so the ~6 us a tile
+// otherwise spent filling its pipeline and storing its output overlaps the
+// neighbouring tiles' loads and MFMAs.
 #include <algorithm>
 
 #include "et_common.hpp"
@@ -73,9 +77,7 @@ constexpr int kThreads = 256;
 constexpr int kGroupM = 8;        // slot tiles per group in the tile order
 constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
 constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
-constexpr int kOutPitch = 2 * kBN + 16;   // bytes per row of the output tile staged in LDS
-constexpr int kOutPitchHalf = kBN + 16;   // the same for the 128-column SwiGLU tile
-constexpr int kSmemBytes = 2 * kStage > kBM * kOutPitch ? 2 * kStage : kBM * kOutPitch;
+constexpr int kSmemBytes = 2 * kStage;
 
 struct GemmArgs {
     const uint16_t* a;              // gather: X [a_rows, K]; else A [cap, K]
@@ -112,6 +114,38 @@ __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t res, uint32_t vo
                  : "memory");
 }
 
+// The same for 4 bytes per lane: lane i's dword lands at lds + 4 * lane.
+__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t res, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(res), "{m0}"(lds) : "memory");
+}
+
+// Output of one 32 x 32 accumulator tile row segment: lane l (kh = l / 32)
+// holds features 8 r + 4 kh + 0..3 of its slot in P[r] (two bf16x2 words),
+// r = 0..3.  v_permlane32_swap exchanges lanes 32..63 of its first operand
+// with lanes 0..31 of its second (lane layout checked on the device): swapping
+// P[2p] with P[2p + 1] leaves lane l with features 16 p + 8 kh + 0..7, which it
+// stores as one 16-byte write at that column (range-checked offset).
+__device__ __forceinline__ void store_row_segment(u32x2_t (&P)[4], __amdgpu_buffer_rsrc_t res, bool row_ok,
+                                                  uint32_t row_base, int col0, int ncols, int kh)
+{
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        u32x2_t& a = P[2 * p];
+        u32x2_t& b = P[2 * p + 1];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const auto r = __builtin_amdgcn_permlane32_swap(a[w], b[w], false, false);
+            a[w] = r[0];
+            b[w] = r[1];
+        }
+        const int col = col0 + 16 * p + 8 * kh;
+        const u32x4_t v = {a[0], a[1], b[0], b[1]};
+        const uint32_t off = (row_ok && col < ncols) ? (row_base + (uint32_t)col) * 2u : kOOR;
+        __builtin_amdgcn_raw_buffer_store_b128(v, res, off, 0, 0);
+    }
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight,
 // then meet the other waves.  The direct-to-LDS loads count in vmcnt and are
 // in LDS once it has dropped, so after the barrier every wave's loads of the
@@ -128,9 +162,10 @@ __device__ __forceinline__ void dma_wait_barrier()
 template <bool GATHER, int EPI>
 __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
 {
-    // the two operand stages, and at the end of a tile the bf16 output tile
+    // the two operand stages
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
+    __shared__ int32_t tokbuf[2][kBM];           // gather: the tokens of a tile's slots, by tile parity
 
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -168,9 +203,40 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int wm = wave >> 1, wn = wave & 1;
     const int nk = (K + kKC - 1) / kKC;
 
-    for (int l = (int)(blockIdx.x >> 3); l < per; l += nloc) {
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
+
+    // Tile context: the block's k-th tile is q = xcd * per + l, l = blockIdx / 8
+    // + k * nloc.  Direct loads of a chunk: wave w fills row groups 8 w + i (i <
+    // 8) of A and of W, rows R = 64 w + 8 i + lane / 8 of the tile; lane puts
+    // segment seg = (lane % 8) ^ key(R) of its row at slot lane % 8, key(R) =
+    // (lane / 8) ^ (i & 1).  Rows past the tile's slots repeat its last slot
+    // (their outputs are not stored); features past N and invalid tokens read 0
+    // (offset marked out of range).
+    int segk[2];              // first k of this lane's segment, by i & 1
+#pragma unroll
+    for (int p = 0; p < 2; ++p) segk[p] = (((lane & 7) ^ (lane >> 3) ^ p)) * 8;
+    struct Tile {
+        bool valid;
+        int64_t s0;           // first slot
+        int rows;             // slots in the tile
+        int n0;               // first output column
+        __amdgpu_buffer_rsrc_t ares, wres;
+    };
+    struct Offsets {
+        uint32_t a[8], b[8];  // per load row: byte offsets of the lane's segment
+    };
+    // First half of a tile's setup: which tile, its descriptors, and (gather)
+    // a direct load of its slots' tokens into tokbuf[buf] (one dword per
+    // lane; slots past the tile read 0 and are never used).  It counts among
+    // the wave's vector-memory operations like the operand loads, so the
+    // waits of the chunk stream cover it.  Second half: the load offsets,
+    // from the tokens in LDS.  Split so that a prefetched tile's offsets are
+    // only computed (and held in registers) once the current tile's own loads
+    // are done.
+    auto setup_a = [&](int l, Tile& t, int buf) {
         const int q = xcd * per + l;
-        if (q >= Q) break;
+        t.valid = l < per && q < Q;
+        if (!t.valid) return;
         // the tile's expert: the last e with ptile[e] <= q / nN
         const int v = q / nN;
         int lo = 0, hi = E;
@@ -187,186 +253,206 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int idx = qq - grp * kGroupM * nN;
         const int mt = grp * kGroupM + idx % gm;
         const int nt = idx / gm;
-        const int64_t s0 = (int64_t)g.expert_offsets[e] + (int64_t)mt * kBM;
+        t.s0 = (int64_t)g.expert_offsets[e] + (int64_t)mt * kBM;
         const int64_t rend = min<int64_t>(g.expert_offsets[e + 1], g.cap);
-        const int rows = (int)min<int64_t>(kBM, rend - s0);
-        const int n0 = nt * (EPI == EPI_SWIGLU ? kBN / 2 : kBN);   // first output column of the tile
-
-        // Direct loads of a chunk: wave w fills row groups 8 w + i (i < 8) of
-        // A and of W, rows R = 64 w + 8 i + lane / 8 of the tile; lane puts
-        // segment seg = (lane % 8) ^ key(R) of its row at slot lane % 8.
-        // key(R) = (lane / 8) ^ (i & 1).  Rows past the tile's slots repeat
-        // its last slot (their outputs are not stored); features past N and
-        // invalid tokens read 0 (offset marked out of range).
-        const __amdgpu_buffer_rsrc_t ares =
-            GATHER ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a), (short)0, (int)(g.a_rows * K * 2),
-                                                       kBufDword3)
-                   : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a + s0 * K), (short)0, rows * K * 2,
-                                                       kBufDword3);
-        const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(g.w + (int64_t)e * N * K), (short)0, N * K * 2, kBufDword3);
-        uint32_t aoff[8], boff[8];
-        int segk[2];              // first k of this lane's segment, by i & 1
-#pragma unroll
-        for (int p = 0; p < 2; ++p) segk[p] = (((lane & 7) ^ (lane >> 3) ^ p)) * 8;
+        t.rows = (int)min<int64_t>(kBM, rend - t.s0);
+        t.n0 = nt * (EPI == EPI_SWIGLU ? kBN / 2 : kBN);
+        t.ares = GATHER ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a), (short)0,
+                                                            (int)(g.a_rows * K * 2), kBufDword3)
+                        : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a + t.s0 * K), (short)0,
+                                                            t.rows * K * 2, kBufDword3);
+        t.wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.w + (int64_t)e * N * K), (short)0,
+                                                   N * K * 2, kBufDword3);
+        if constexpr (GATHER) {
+            const __amdgpu_buffer_rsrc_t tres = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<int32_t*>(g.sorted_token + t.s0), (short)0, t.rows * 4, kBufDword3);
+            dma_b32(tres, (uint32_t)(64 * wave + lane) * 4u,
+                    (uint32_t)(uintptr_t)(lds_t*)&tokbuf[buf][64 * wave]);
+        }
+    };
+    // z is 0; a laundered z (opaque to the compiler) makes it compute the
+    // offsets again instead of keeping an earlier copy in registers.
+    auto setup_b = [&](const Tile& t, Offsets& o, uint32_t z, int buf) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int R = 64 * wave + 8 * i + (lane >> 3);
-            const uint32_t seg = (uint32_t)segk[i & 1] * 2u;
-            const int row = min(R, rows - 1);
+            const uint32_t seg = (uint32_t)segk[i & 1] * 2u + z;
             if constexpr (GATHER) {
-                const int tok = g.sorted_token[s0 + row];
-                aoff[i] = (uint32_t)tok < (uint32_t)g.a_rows ? (uint32_t)tok * (uint32_t)K * 2u + seg : kOOR;
+                const uint32_t tok = (uint32_t)tokbuf[buf][min(R, t.rows - 1)];
+                o.a[i] = tok < (uint32_t)g.a_rows ? tok * (uint32_t)K * 2u + seg : kOOR;
             } else {
-                aoff[i] = (uint32_t)row * (uint32_t)K * 2u + seg;
+                o.a[i] = (uint32_t)min(R, t.rows - 1) * (uint32_t)K * 2u + seg;
             }
             if constexpr (EPI == EPI_SWIGLU) {
                 // tile row R -> wave column half R / 128, MFMA tile (R / 32) % 4
                 // (0, 1: gate; 2, 3: up), so a wave's gate and up accumulators
                 // of one hidden unit sit in the same lane and register
-                const int t = (R >> 5) & 3;
-                const int hid = n0 + (R >> 7) * 64 + (t & 1) * 32 + (R & 31);
-                boff[i] = hid < F ? (uint32_t)(t >= 2 ? F + hid : hid) * (uint32_t)K * 2u + seg : kOOR;
+                const int tt = (R >> 5) & 3;
+                const int hid = t.n0 + (R >> 7) * 64 + (tt & 1) * 32 + (R & 31);
+                o.b[i] = hid < F ? (uint32_t)(tt >= 2 ? F + hid : hid) * (uint32_t)K * 2u + seg : kOOR;
             } else {
-                const int n = n0 + R;
-                boff[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
+                const int n = t.n0 + R;
+                o.b[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
             }
         }
-        const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
-        // chunk c -> stage c & 1; the chunk's column offset c * 128 bytes
-        // goes in the scalar offset.  A chunk that runs past K masks the
-        // segments at or past K (K is a multiple of 8, so a segment is all
-        // in or all out).
-        // One direct load of chunk c: q even -> A block q / 2, q odd -> W block
-        // q / 2.  A chunk that runs past K masks the segments at or past K
-        // (K is a multiple of 8, so a segment is all in or all out).
-        auto dma_one = [&](int c, int q) {
-            const int i = q >> 1;
-            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u + (uint32_t)i * 1024u;
-            const uint32_t soff = (uint32_t)c * 128u;
-            const uint32_t kmask = (c + 1) * kKC <= K || c * kKC + segk[i & 1] < K ? 0u : kOOR;
-            if (q & 1) dma_b128(wres, boff[i] | kmask, soff, sb + kHalf);
-            else dma_b128(ares, aoff[i] | kmask, soff, sb);
-        };
-        auto issue = [&](int c) {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) dma_one(c, q);
-        };
+    };
 
-        f32x16_t acc[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    // The block's tiles form one stream of chunks: chunk c of a tile goes to
+    // stage (c + par) & 1, and the next tile's parity follows on (par += nk).
+    // One direct load of a tile's chunk c: q even -> A block q / 2, q odd -> W
+    // block q / 2.  A chunk that runs past K masks the segments at or past K
+    // (K is a multiple of 8, so a segment is all in or all out).
+    auto dma_one = [&](const Tile& t, const Offsets& o, int c, int par, int q) {
+        const int i = q >> 1;
+        const uint32_t sb =
+            lds0 + (uint32_t)((c + par) & 1) * kStage + (uint32_t)wave * 8192u + (uint32_t)i * 1024u;
+        const uint32_t soff = (uint32_t)c * 128u;
+        const uint32_t kmask = (c + 1) * kKC <= K || c * kKC + segk[i & 1] < K ? 0u : kOOR;
+        if (q & 1) dma_b128(t.wres, o.b[i] | kmask, soff, sb + kHalf);
+        else dma_b128(t.ares, o.a[i] | kmask, soff, sb);
+    };
 
-        // Fragment of tile t (32 rows), k-step ks: lane l reads row R = 32 t +
-        // l % 32, segment 2 ks + l / 32, at 1024 (R / 8) + 128 (R % 8) +
-        // 16 ((2 ks + l / 32) ^ key(R)); key(R) = (l % 8) ^ ((l / 8) & 1).
-        const int fkey = (lane & 7) ^ ((lane >> 3) & 1);
-        const int flane = ((lane & 31) >> 3) * 1024 + (lane & 7) * 128;
-        const unsigned char* const abase = smem + wm * 16384 + flane;
-        const unsigned char* const bbase = smem + kHalf + wn * 16384 + flane;
-        u32x4_t f[4][2][4];       // [k-step][A, W][tile]: a whole chunk's fragments
-        // fragment q of k-step ks (q < 4: A tile q, else W tile q - 4)
-        auto frag_one = [&](int c, int ks, int q) {
-            const int off = (c & 1) * kStage + (((2 * ks + (lane >> 5)) ^ fkey) << 4) + (q & 3) * 4096;
-            f[ks][q >> 2][q & 3] = *reinterpret_cast<const u32x4_t*>((q < 4 ? abase : bbase) + off);
-        };
-        auto read_frags = [&](int c, int ks) {
+    f32x16_t acc[4][4];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) frag_one(c, ks, q);
-        };
-        // MFMA m of k-step ks: slot tile m / 4, feature tile m % 4
-        auto mfma_one = [&](int ks, int m) {
-            const int i = m >> 2, j = m & 3;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
-                                                                __builtin_bit_cast(bf16x8_t, f[ks][0][i]), acc[i][j],
-                                                                0, 0, 0);
-        };
-        auto pin = [&]() { __builtin_amdgcn_sched_barrier(0); };
-        auto barrier = [&]() {
-            pin();
-            asm volatile("s_barrier" ::: "memory");
-            pin();
-        };
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
-        // Every wave has finished reading the previous tile's stages (its
-        // last fragment reads were consumed by its MFMAs), and the epilogue's
-        // LDS reads were consumed by its stores.  Only the previous tile's
-        // stores can be in flight; the first wait below counts them with the
-        // loads, since vmcnt retires in issue order.
-        barrier();
-        issue(0);
-        if (nk > 1) issue(1);
-        if (nk > 1) dma_wait_barrier<16>();
-        else dma_wait_barrier<0>();
-        read_frags(0, 0);
-        read_frags(0, 1);
-        read_frags(0, 2);
-        // Step c (chunk c in stage c & 1, its k-steps 0..2 already in
-        // registers).  Each wave reads the chunk's last k-step, so once it
-        // has waited for its reads and met the others, nobody reads stage
-        // c & 1 any more: chunk c + 2 is loaded into it while k-steps 1 and 2
-        // multiply.  Then every wave waits for chunk c + 1 (chunk c + 2's 16
-        // loads per wave may stay in flight), meets the others, and reads
-        // chunk c + 1's k-steps 0..2 under k-step 3's MFMAs.  So two chunks
-        // stream in while one is multiplied, with two LDS stages.  A wave
-        // issues in order, so every load and fragment read sits between two
-        // MFMAs (the order is pinned): the matrix pipe keeps a queued MFMA
-        // while they issue.
-        for (int c = 0; c < nk; ++c) {
-#pragma unroll
-            for (int m = 0; m < 16; ++m) {
-                mfma_one(0, m);
-                pin();
-                if (m < 8) frag_one(c, 3, m);
-                pin();
-            }
-            // (the builtin, not inline assembly: the compiler then knows these
-            // reads are complete and adds no waits for them later)
-            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-            barrier();
-            const bool more2 = c + 2 < nk;
-#pragma unroll
-            for (int m = 0; m < 32; ++m) {
-                mfma_one(1 + (m >> 4), m & 15);
-                pin();
-                if (more2 && (m & 1)) dma_one(c + 2, m >> 1);
-                pin();
-            }
-            const bool more1 = c + 1 < nk;
-            if (more1) {
-                if (more2) dma_wait_barrier<16>();
-                else dma_wait_barrier<0>();
-            }
-#pragma unroll
-            for (int m = 0; m < 16; ++m) {
-                mfma_one(3, m);
-                pin();
-                if (more1) {
-                    const int r0 = (3 * m) / 2, r1 = (3 * m + 3) / 2;   // 24 reads over 16 MFMAs
-                    for (int r = r0; r < r1; ++r) frag_one(c + 1, r >> 3, r & 7);
-                }
-                pin();
-            }
-        }
-
-        // Epilogue, through LDS so that the stores are whole rows: every wave
-        // has issued its last MFMAs (their fragment reads are done), so after
-        // a barrier the stages are free.  Lane l holds slot (wm * 4 + i) * 32 +
-        // l % 32 and tile columns (wn * 4 + j) * 32 + 8 r + 4 (l / 32) + 0..3
-        // in acc[i][j][4 r ..].  The bf16 results go to an LDS tile of 256
-        // rows (16 bytes of padding per row put the 32 rows of one write on
-        // distinct banks).  Then each wave stores 64 rows, whole rows per
-        // instruction, with range-checked stores: rows past the tile's slots
-        // and columns past the output get an out-of-range offset and are
-        // dropped.
-        __builtin_amdgcn_sched_barrier(0);
+    // Fragment of tile t (32 rows), k-step ks: lane l reads row R = 32 t +
+    // l % 32, segment 2 ks + l / 32, at 1024 (R / 8) + 128 (R % 8) +
+    // 16 ((2 ks + l / 32) ^ key(R)); key(R) = (l % 8) ^ ((l / 8) & 1).
+    const int fkey = (lane & 7) ^ ((lane >> 3) & 1);
+    const int flane = ((lane & 31) >> 3) * 1024 + (lane & 7) * 128;
+    const unsigned char* const abase = smem + wm * 16384 + flane;
+    const unsigned char* const bbase = smem + kHalf + wn * 16384 + flane;
+    u32x4_t f[4][2][4];       // [k-step][A, W][tile]: a whole chunk's fragments
+    // fragment q of k-step ks of the chunk in stage st (q < 4: A tile q, else
+    // W tile q - 4)
+    auto frag_one = [&](int st, int ks, int q) {
+        const int off = st * kStage + (((2 * ks + (lane >> 5)) ^ fkey) << 4) + (q & 3) * 4096;
+        f[ks][q >> 2][q & 3] = *reinterpret_cast<const u32x4_t*>((q < 4 ? abase : bbase) + off);
+    };
+    // MFMA m of k-step ks: slot tile m / 4, feature tile m % 4
+    auto mfma_one = [&](int ks, int m) {
+        const int i = m >> 2, j = m & 3;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
+                                                            __builtin_bit_cast(bf16x8_t, f[ks][0][i]), acc[i][j],
+                                                            0, 0, 0);
+    };
+    auto pin = [&]() { __builtin_amdgcn_sched_barrier(0); };
+    auto barrier = [&]() {
+        pin();
         asm volatile("s_barrier" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        // The accumulators stay in the accumulation registers up to here (the
-        // epilogues' arithmetic would otherwise lead the register allocator to
-        // keep some in the vector registers the K loop needs).
+        pin();
+    };
+
+    Tile cur, nxt;
+    Offsets co, no;           // load offsets of the current and the next tile
+    int l = (int)(blockIdx.x >> 3);
+    int buf = 0;              // tokbuf of the current tile
+    setup_a(l, cur, buf);
+    if (!cur.valid) return;
+    if (GATHER) dma_wait_barrier<0>();
+    setup_b(cur, co, 0u, buf);
+    int par = 0;              // stage of chunk c: (c + par) & 1
+    // First tile: chunks 0 and 1 in flight, wait for chunk 0, read its
+    // k-steps 0..2.  Later tiles find theirs prefetched (below).
+    {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) dma_one(cur, co, 0, par, q);
+        if (nk > 1) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) dma_one(cur, co, 1, par, q);
+            dma_wait_barrier<16>();
+        } else {
+            dma_wait_barrier<0>();
+        }
+#pragma unroll
+        for (int q = 0; q < 24; ++q) frag_one(par & 1, q >> 3, q & 7);
+    }
+    // With two chunks or more per tile, the last two chunks of a tile load the
+    // next tile's chunks 0 and 1, so a tile starts with its data in LDS and the
+    // previous tile's stores overlap its loads.
+    const bool stream = nk >= 2;
+    // Step c (chunk c in stage (c + par) & 1, its k-steps 0..2 already in
+    // registers).  Each wave reads the chunk's last k-step, so once it has
+    // waited for its reads and met the others, nobody reads that stage any
+    // more: the stream's chunk two ahead is loaded into it (load(q), q < 16)
+    // while k-steps 1 and 2 multiply.  Then every wave waits for the stream's
+    // next chunk (the one after may stay in flight), meets the others, and
+    // reads its k-steps 0..2 under k-step 3's MFMAs -- within the tile; the
+    // next tile's first fragments are read after the epilogue.  Every load and
+    // fragment read sits between two MFMAs (the order is pinned): the matrix
+    // pipe keeps a queued MFMA while they issue.
+    auto step = [&](int c, auto load, bool more2, bool more1) {
+        const int st = (c + par) & 1;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            mfma_one(0, m);
+            pin();
+            if (m < 8) frag_one(st, 3, m);
+            pin();
+        }
+        // (the builtin, not inline assembly: the compiler then knows these
+        // reads are complete and adds no waits for them later)
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        barrier();
+#pragma unroll
+        for (int m = 0; m < 32; ++m) {
+            mfma_one(1 + (m >> 4), m & 15);
+            pin();
+            if (more2 && (m & 1)) load(m >> 1);
+            pin();
+        }
+        if (more1) {
+            if (more2) dma_wait_barrier<16>();
+            else dma_wait_barrier<0>();
+        }
+        const int st1 = st ^ 1;                    // the stream's next chunk
+        const bool rd1 = c + 1 < nk;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            mfma_one(3, m);
+            pin();
+            if (rd1) {
+                const int r0 = (3 * m) / 2, r1 = (3 * m + 3) / 2;   // 24 reads over 16 MFMAs
+                for (int r = r0; r < r1; ++r) frag_one(st1, r >> 3, r & 7);
+            }
+            pin();
+        }
+    };
+
+    for (;;) {
+        l += nloc;
+        setup_a(l, nxt, buf ^ 1);
+        const bool more_tiles = nxt.valid && stream;
+        // chunks whose stream successor two ahead is this tile's own
+        const int nmain = nk - 2;
+        for (int c = 0; c < nmain; ++c)
+            step(c, [&](int q) { dma_one(cur, co, c + 2, par, q); }, true, true);
+        // the last two chunks: the stream's chunks two ahead are the next
+        // tile's 0 and 1
+        // (the next tile's tokens: its token load is older than the stream's
+        // last 16 loads, so any chunk wait of the loop above covered it; with
+        // no such wait, wait here)
+        if (more_tiles) {
+            if (GATHER && nmain <= 0) dma_wait_barrier<0>();
+            setup_b(nxt, no, 0u, buf ^ 1);
+        }
+        for (int c = max(nmain, 0); c < nk; ++c)
+            step(c, [&](int q) { dma_one(nxt, no, c + 2 - nk, par + nk, q); }, more_tiles,
+                 c + 1 < nk || more_tiles);
+
+        // Epilogue straight from the accumulators: lane l holds slot (wm * 4 +
+        // i) * 32 + l % 32 and tile columns (wn * 4 + j) * 32 + 8 r + 4 (l / 32)
+        // + 0..3 in acc[i][j][4 r ..]; pairs of lanes swap halves so that each
+        // stores 16 bytes through a range-checked descriptor (rows past the
+        // tile's slots and columns past the output get an out-of-range offset
+        // and are dropped).  The
+        // LDS stages keep the next tile's chunks meanwhile.  The accumulators
+        // stay in the accumulation registers up to here (the epilogues'
+        // arithmetic would otherwise lead the register allocator to keep some
+        // in the vector registers the K loop needs).
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -375,40 +461,33 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             // h = (g * sigmoid(g)) * u in binary32, from the gate tiles j = 0, 1
             // and the up tiles j + 2 of the same lane and register; 128 hidden
             // columns per tile, wave column half wn holds hidden wn * 64 ...
-            // (one slot tile at a time keeps the sigmoid temporaries few; the
-            // loop stays unrolled so that the accumulators are indexed statically)
+            const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(
+                g.c + cur.s0 * F, (short)0, cur.rows * F * 2, kBufDword3);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                __builtin_amdgcn_sched_barrier(0);
-                unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitchHalf;
+                __builtin_amdgcn_sched_barrier(0);       // one slot tile at a time: few temporaries
+                const int row = (wm * 4 + i) * 32 + r32;
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < 2; ++j) {
+                    u32x2_t P[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        __builtin_amdgcn_sched_barrier(0);   // one 4-value group at a time
                         float h[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float gv = acc[i][j][4 * r + e];
                             h[e] = (gv * sigmoid(gv)) * acc[i][j + 2][4 * r + e];
                         }
-                        const int col = wn * 64 + j * 32 + 8 * r + 4 * kh;
-                        const u32x2_t val = {pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-                        *reinterpret_cast<u32x2_t*>(orow + col * 2) = val;
+                        P[r] = u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
                     }
-            }
-            __syncthreads();
-            const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * F, (short)0,
-                                                                                   rows * F * 2, kBufDword3);
-            const int n = n0 + (lane & 15) * 8;
-#pragma unroll 4
-            for (int q = 0; q < 16; ++q) {
-                const int row = wave * 64 + 4 * q + (lane >> 4);
-                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * kOutPitchHalf + (lane & 15) * 16);
-                const uint32_t off =
-                    (row < rows && n < F) ? ((uint32_t)row * (uint32_t)F + (uint32_t)n) * 2u : kOOR;
-                __builtin_amdgcn_raw_buffer_store_b128(v, cres, off, 0, 0);
+                    store_row_segment(P, cres, row < cur.rows, (uint32_t)row * (uint32_t)F,
+                                      cur.n0 + wn * 64 + j * 32, F, kh);
+                }
             }
         } else {
+            const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(
+                g.c + cur.s0 * N, (short)0, cur.rows * N * 2, kBufDword3);
             // (the compiler barrier keeps the row-scale loads here rather than
             // hoisted above the K loop, where their registers would be live)
             asm volatile("" ::: "memory");
@@ -418,39 +497,59 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                 sc[i] = 1.0f;
                 if constexpr (EPI == EPI_ROW_SCALE) {
                     const int row = (wm * 4 + i) * 32 + r32;
-                    sc[i] = g.row_scale[s0 + min(row, rows - 1)];
+                    sc[i] = g.row_scale[cur.s0 + min(row, cur.rows - 1)];
                 }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if constexpr (EPI == EPI_ROW_SCALE) __builtin_amdgcn_sched_barrier(0);   // one slot tile at a time
-                unsigned char* const orow = smem + ((wm * 4 + i) * 32 + r32) * kOutPitch;
+                const int row = (wm * 4 + i) * 32 + r32;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j) {
+                    __builtin_amdgcn_sched_barrier(0);       // one 32 x 32 tile at a time
+                    u32x2_t P[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float v[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             v[e] = EPI == EPI_ROW_SCALE ? sc[i] * acc[i][j][4 * r + e] : acc[i][j][4 * r + e];
-                        const int col = (wn * 4 + j) * 32 + 8 * r + 4 * kh;
-                        const u32x2_t val = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                        *reinterpret_cast<u32x2_t*>(orow + col * 2) = val;
+                        P[r] = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     }
-            }
-            __syncthreads();
-            const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(g.c + s0 * N, (short)0,
-                                                                                   rows * N * 2, kBufDword3);
-            const int n = n0 + (lane & 31) * 8;
-#pragma unroll 4
-            for (int q = 0; q < 32; ++q) {
-                const int row = wave * 64 + 2 * q + kh;
-                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * kOutPitch + (lane & 31) * 16);
-                const uint32_t off =
-                    (row < rows && n < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)n) * 2u : kOOR;
-                __builtin_amdgcn_raw_buffer_store_b128(v, cres, off, 0, 0);
+                    store_row_segment(P, cres, row < cur.rows, (uint32_t)row * (uint32_t)N,
+                                      cur.n0 + (wn * 4 + j) * 32, N, kh);
+                }
             }
         }
+        if (!nxt.valid) break;
+        // (nothing below moves into the epilogue, where it would hold registers)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+        if (!stream) {
+            // one chunk per tile: load it now (every wave has finished reading
+            // the stage: its reads were consumed by its MFMAs, and the
+            // barrier makes that hold for all waves)
+            dma_wait_barrier<0>();
+            setup_b(nxt, no, 0u, buf ^ 1);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) dma_one(nxt, no, 0, par + nk, q);
+            dma_wait_barrier<0>();
+        }
+        // the next tile's chunk 0 is in its stage for every wave (the last
+        // step's wait and barrier, or the one just above): its k-steps 0..2
+#pragma unroll
+        for (int q = 0; q < 24; ++q) frag_one((par + nk) & 1, q >> 3, q & 7);
+        par = (par + nk) & 1;
+        cur = nxt;
+        buf ^= 1;
+        // the offsets again, from the tokens in LDS (nothing was kept in
+        // registers across the epilogue)
+        uint32_t z = 0u;
+        asm volatile("" : "+v"(z));
+        setup_b(cur, co, z, buf);
     }
 }
 
