@@ -43,9 +43,10 @@
 // CU).  Each block computes the per-expert tile prefix once, then walks its
 // tiles.  The 8 XCDs take blocks in turn (block b runs on XCD b % 8), so XCD
 // x is given the contiguous range of tiles [x * per, (x + 1) * per); inside an
-// expert, tiles are ordered in groups of 8 slot tiles x every feature tile, so
-// the ~32 blocks running together on one XCD share 8 A tiles and 4 W tiles
-// through that XCD's L2.  A block's tiles form one stream of chunks: the last
+// expert, tiles are ordered in groups of 4 slot tiles x every feature tile, so
+// the ~32 blocks running together on one XCD share 4 A tiles and 8 W tiles
+// through that XCD's L2 (the larger A is fetched again less often; an
+// expert's W is re-read from the last-level cache).  A block's tiles form one stream of chunks: the last
 // two chunks of a tile load the next tile's first two, so the ~6 us a tile
 // otherwise spent filling its pipeline and storing its output overlaps the
 // neighbouring tiles' loads and MFMAs.
@@ -74,7 +75,7 @@ constexpr int kBM = 256;          // slots per tile
 constexpr int kBN = 256;          // output features per tile
 constexpr int kKC = 64;           // k per chunk (four k-steps of 16): 128 bytes of a row
 constexpr int kThreads = 256;
-constexpr int kGroupM = 8;        // slot tiles per group in the tile order
+constexpr int kGroupM = 4;        // slot tiles per group in the tile order
 constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
 constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
 constexpr int kSmemBytes = 2 * kStage;
