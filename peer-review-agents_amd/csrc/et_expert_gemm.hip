@@ -828,20 +828,25 @@ __global__ __launch_bounds__(kThreads) void expert_wgrad_kernel(WgradArgs g)
             aoff[i] = k < K ? ((uint32_t)r * (uint32_t)K + (uint32_t)k) * 2u : kOOR;
         }
         // chunk c: slots lo + 64 c ..; descriptors rebased per chunk, so slots
-        // past the expert's read 0
-        auto issue = [&](int c) {
+        // past the expert's read 0.  Load q of a chunk: row pair q / 2, dc for
+        // q even, a for q odd.
+        auto dma_one = [&](int c, int q) {
             const int64_t s0 = lo + 64 * (int64_t)c;
             const int nrow = min(64, (int)(hi - s0));
-            const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(g.dc + s0 * N), (short)0, nrow * N * 2, kBufDword3);
-            const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(g.a + s0 * K), (short)0, nrow * K * 2, kBufDword3);
-            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                dma_b128(dres, doff[i], 0u, sb + i * 1024);
-                dma_b128(ares, aoff[i], 0u, sb + kHalf + i * 1024);
+            const uint32_t sb = lds0 + (uint32_t)(c & 1) * kStage + (uint32_t)wave * 8192u + (uint32_t)(q >> 1) * 1024u;
+            if (q & 1) {
+                const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint16_t*>(g.a + s0 * K), (short)0, nrow * K * 2, kBufDword3);
+                dma_b128(ares, aoff[q >> 1], 0u, sb + kHalf);
+            } else {
+                const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint16_t*>(g.dc + s0 * N), (short)0, nrow * N * 2, kBufDword3);
+                dma_b128(dres, doff[q >> 1], 0u, sb);
             }
+        };
+        auto issue = [&](int c) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) dma_one(c, q);
         };
 
         f32x16_t acc[4][4];
@@ -851,66 +856,80 @@ __global__ __launch_bounds__(kThreads) void expert_wgrad_kernel(WgradArgs g)
             for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
         u32x4_t f[4][2][4];       // [k-step][dc, a][tile]
-        auto read_frags = [&](int c, int ks) {
+        // read r of k-step ks (r < 16): operand r / 8, tile (r / 2) % 4, half
+        // r % 2 (rows 4 h .. 4 h + 3 of the lane's 8) -> that half of the
+        // fragment
+        auto read_one = [&](int c, int ks, int r) {
+            const int o = r >> 3, t = (r >> 1) & 3, h = r & 1;
             const unsigned char* st = smem + (c & 1) * kStage + ks * 16 * 512;
-#pragma unroll
-            for (int o = 0; o < 2; ++o)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint2 h0 = read_tr16(st + fb[o][t]);
-                    const uint2 h1 = read_tr16(st + fb[o][t] + 4 * 512);
-                    f[ks][o][t] = u32x4_t{h0.x, h0.y, h1.x, h1.y};
-                }
+            const uint2 v = read_tr16(st + fb[o][t] + h * 4 * 512);
+            if (h == 0) {
+                f[ks][o][t][0] = v.x;
+                f[ks][o][t][1] = v.y;
+            } else {
+                f[ks][o][t][2] = v.x;
+                f[ks][o][t][3] = v.y;
+            }
         };
-        auto mfmas = [&](int ks) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][0][i]),
-                                                                        __builtin_bit_cast(bf16x8_t, f[ks][1][j]),
-                                                                        acc[i][j], 0, 0, 0);
+        // MFMA m of k-step ks: dc tile m / 4, a tile m % 4
+        auto mfma_one = [&](int ks, int m) {
+            const int i = m >> 2, j = m & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][0][i]),
+                                                                __builtin_bit_cast(bf16x8_t, f[ks][1][j]),
+                                                                acc[i][j], 0, 0, 0);
         };
+        auto pin = [&]() { __builtin_amdgcn_sched_barrier(0); };
         auto barrier = [&]() {
-            __builtin_amdgcn_sched_barrier(0);
+            pin();
             asm volatile("s_barrier" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
+            pin();
         };
 
-        // Same schedule as the forward kernel: a whole chunk's fragments in
-        // registers, two chunks streaming while one is multiplied.
+        // The forward kernel's schedule: a whole chunk's fragments in
+        // registers, two chunks streaming while one is multiplied, and every
+        // load and fragment read between two MFMAs (the order pinned).
         barrier();
         if (nk > 0) {
             issue(0);
             if (nk > 1) issue(1);
             if (nk > 1) dma_wait_barrier<16>();
             else dma_wait_barrier<0>();
-            read_frags(0, 0);
-            read_frags(0, 1);
-            read_frags(0, 2);
+#pragma unroll
+            for (int r = 0; r < 48; ++r) read_one(0, r >> 4, r & 15);
         }
         for (int c = 0; c < nk; ++c) {
-            read_frags(c, 3);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(0);
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                mfma_one(0, m);
+                pin();
+                read_one(c, 3, m);
+                pin();
+            }
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
             barrier();
-            if (c + 2 < nk) issue(c + 2);
-            mfmas(1);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(2);
-            __builtin_amdgcn_sched_barrier(0);
-            if (c + 1 < nk) {
-                if (c + 2 < nk) dma_wait_barrier<16>();
-                else dma_wait_barrier<0>();
-                read_frags(c + 1, 0);
-                read_frags(c + 1, 1);
-                read_frags(c + 1, 2);
+            const bool more2 = c + 2 < nk;
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                mfma_one(1 + (m >> 4), m & 15);
+                pin();
+                if (more2 && (m & 1)) dma_one(c + 2, m >> 1);
+                pin();
             }
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(3);
-            __builtin_amdgcn_sched_barrier(0);
+            const bool more1 = c + 1 < nk;
+            if (more1) {
+                if (more2) dma_wait_barrier<16>();
+                else dma_wait_barrier<0>();
+            }
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                mfma_one(3, m);
+                pin();
+                if (more1) {
+#pragma unroll
+                    for (int r = 3 * m; r < 3 * m + 3; ++r) read_one(c + 1, r >> 4, r & 15);   // 48 reads
+                }
+                pin();
+            }
         }
 
         // Epilogue: f32 straight from the accumulators, 128-byte row pieces.
