@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 6
+#define ET_ABI_VERSION 7
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -282,6 +282,28 @@ int et_router_route(const void* x, const void* w, const float* thr, int64_t num_
 int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
                    const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
                    int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream);
+
+/*
+ * The expert grouped GEMM on fp8 operands, on gfx950's fp8 matrix cores (twice
+ * the bf16 rate):
+ *   c[s, n] = ((sum_k a[row(s), k] * w[e(s), n, k]) * a_scale[row(s)]) * w_scale[e(s), n]
+ * with a and w in OCP fp8 e4m3 (one byte per element), their products summed
+ * in binary32 in ascending k-steps of 64 (one MFMA each, unit block scales),
+ * the two scale products rounded in the order written, and one rounding to
+ * bf16.  row(s), the modes (gather with sorted_token, or slot-major with
+ * NULL), slot_capacity and the output are those of et_expert_gemm; a_scale
+ * [a_rows] f32 scales each row of a (a token in gather mode), w_scale [E, N]
+ * f32 each weight row.  epilogue: ET_GEMM_PLAIN or ET_GEMM_SWIGLU (h =
+ * (g * sigmoid(g)) * u of the scaled gate and up values).  K a multiple of 16
+ * below 2^22, N a multiple of 8 (16 for SwiGLU), N*K below 2^31; a, w, c and
+ * w_scale 16-byte aligned, a_scale 4-byte aligned.  Integer-valued operands
+ * with power-of-two scales and partial sums below 2^24 give the exact
+ * product before the bf16 rounding.  Implements an fp8 form of the expert
+ * GEMM that consumes the dispatch (no reference counterpart).
+ */
+int et_expert_gemm_fp8(const void* a, int64_t a_rows, const float* a_scale, const int32_t* sorted_token,
+                       const void* w, const float* w_scale, const int32_t* expert_offsets, int64_t num_experts,
+                       int64_t K, int64_t N, int64_t slot_capacity, int epilogue, void* c, void* stream);
 
 /*
  * Weight transpose for the expert GEMM's input gradient:

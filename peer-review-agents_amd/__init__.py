@@ -16,6 +16,7 @@ from .expert_threshold import (  # noqa: F401
     dispatch_autograd,
     dispatch_backward,
     expert_gemm,
+    expert_gemm_fp8,
     expert_gemm_input_grad,
     expert_gemm_weight_grad,
     expert_weight_transpose,

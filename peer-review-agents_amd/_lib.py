@@ -61,6 +61,7 @@ _SIGNATURES = {
     "et_router_wgrad_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "et_router_wgrad": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _sz, _p]),
     "et_expert_gemm": (_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _p, _p]),
+    "et_expert_gemm_fp8": (_int, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _p]),
     "et_expert_weight_transpose": (_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "et_expert_wgrad": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "et_swiglu_fwd": (_int, [_p, _i64, _p, _i64, _i64, _p, _p]),

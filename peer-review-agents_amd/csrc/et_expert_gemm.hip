@@ -51,6 +51,7 @@
 // otherwise spent filling its pipeline and storing its output overlaps the
 // neighbouring tiles' loads and MFMAs.
 #include <algorithm>
+#include <type_traits>
 
 #include "et_common.hpp"
 
@@ -61,6 +62,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_t;
 
 // Word 3 of a gfx9 buffer descriptor for raw (untyped, stride 0) access.
@@ -81,12 +84,14 @@ constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
 constexpr int kSmemBytes = 2 * kStage;
 
 struct GemmArgs {
-    const uint16_t* a;              // gather: X [a_rows, K]; else A [cap, K]
+    const unsigned char* a;         // gather: X [a_rows, K]; else A [cap, K] (bf16, or fp8 e4m3)
     const int32_t* sorted_token;    // [cap] (gather only)
-    const uint16_t* w;              // [E, N, K]
+    const unsigned char* w;         // [E, N, K] (bf16, or fp8 e4m3)
     const int32_t* expert_offsets;  // [E + 1]
-    uint16_t* c;                    // [cap, N]
+    uint16_t* c;                    // [cap, N] bf16
     const float* row_scale;         // [cap] (EPI_ROW_SCALE only)
+    const float* a_scale;           // fp8: [a_rows], the scale of each row of a
+    const float* w_scale;           // fp8: [E, N], the scale of each weight row
     int64_t a_rows;
     int64_t cap;
     int K, N, E;                    // N: rows of each expert's weight (2 F for SwiGLU)
@@ -160,13 +165,26 @@ __device__ __forceinline__ void dma_wait_barrier()
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool GATHER, int EPI>
+// FP8: operands in OCP fp8 e4m3 (one byte per element) on
+// v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales, and the products
+// scaled by a_scale[row] * w_scale[e, n] in the epilogue.  A chunk row is the
+// same 128 bytes, so a chunk holds 128 k in two k-steps of 64; lane l's
+// fragment is row l % 32, the 32 bytes at 32 (l / 32) of the k-step (two
+// 16-byte segments).  The MFMA's sum over a k-step is the same for any
+// permutation of k applied to both operands (checked on the device), so the
+// fragment layouts of A and W only have to agree.
+template <bool GATHER, int EPI, bool FP8 = false>
 __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
 {
+    constexpr int ES = FP8 ? 1 : 2;           // bytes per element
+    constexpr int KC = 128 / ES;              // k per chunk (one 128-byte row)
+    constexpr int NKS = FP8 ? 2 : 4;          // k-steps per chunk
     // the two operand stages
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
     __shared__ int32_t tokbuf[2][kBM];           // gather: the tokens of a tile's slots, by tile parity
+    __shared__ float wsbuf[2][kBN];              // fp8: the weight-row scales of a tile's columns, by parity
+    __shared__ float asbuf[2][kBM];              // fp8: the scales of a tile's rows of a, by parity
 
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -202,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int r32 = lane & 31;
     const int kh = lane >> 5;
     const int wm = wave >> 1, wn = wave & 1;
-    const int nk = (K + kKC - 1) / kKC;
+    const int nk = (K + KC - 1) / KC;
 
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_t*)smem;
 
@@ -215,16 +233,17 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // (offset marked out of range).
     int segk[2];              // first k of this lane's segment, by i & 1
 #pragma unroll
-    for (int p = 0; p < 2; ++p) segk[p] = (((lane & 7) ^ (lane >> 3) ^ p)) * 8;
+    for (int p = 0; p < 2; ++p) segk[p] = (((lane & 7) ^ (lane >> 3) ^ p)) * (16 / ES);
     struct Tile {
         bool valid;
         int64_t s0;           // first slot
         int rows;             // slots in the tile
         int n0;               // first output column
+        int e;                // expert
         __amdgpu_buffer_rsrc_t ares, wres;
     };
     struct Offsets {
-        uint32_t a[8], b[8];  // per load row: byte offsets of the lane's segment
+        uint32_t a[8];        // gather: per load row, the byte offset of the lane's segment
     };
     // First half of a tile's setup: which tile, its descriptors, and (gather)
     // a direct load of its slots' tokens into tokbuf[buf] (one dword per
@@ -258,12 +277,13 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int64_t rend = min<int64_t>(g.expert_offsets[e + 1], g.cap);
         t.rows = (int)min<int64_t>(kBM, rend - t.s0);
         t.n0 = nt * (EPI == EPI_SWIGLU ? kBN / 2 : kBN);
-        t.ares = GATHER ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a), (short)0,
-                                                            (int)(g.a_rows * K * 2), kBufDword3)
-                        : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.a + t.s0 * K), (short)0,
-                                                            t.rows * K * 2, kBufDword3);
-        t.wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.w + (int64_t)e * N * K), (short)0,
-                                                   N * K * 2, kBufDword3);
+        t.e = e;
+        t.ares = GATHER ? __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(g.a), (short)0,
+                                                            (int)(g.a_rows * K * ES), kBufDword3)
+                        : __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(g.a + t.s0 * K * ES),
+                                                            (short)0, t.rows * K * ES, kBufDword3);
+        t.wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(g.w + (int64_t)e * N * K * ES),
+                                                   (short)0, N * K * ES, kBufDword3);
         if constexpr (GATHER) {
             const __amdgpu_buffer_rsrc_t tres = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<int32_t*>(g.sorted_token + t.s0), (short)0, t.rows * 4, kBufDword3);
@@ -271,30 +291,87 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                     (uint32_t)(uintptr_t)(lds_t*)&tokbuf[buf][64 * wave]);
         }
     };
+    // fp8: direct loads of a tile's scales into wsbuf[buf] and asbuf[buf],
+    // one dword per lane: its 256 weight-row scales in output-column order
+    // (SwiGLU: 128 gate rows, then their 128 up rows; columns past the weight
+    // read 0) and the scales of its 256 rows of a (by token in gather mode;
+    // the tokens must have landed in tokbuf[buf]; rows past the tile's slots
+    // and invalid tokens read 0).  Issued only after a barrier that follows
+    // the previous tile's epilogue, the last reader of these buffers.
+    auto setup_scales = [&](const Tile& t, int buf) {
+        if constexpr (FP8) {
+            const int ent = 64 * wave + lane;
+            int n;
+            if constexpr (EPI == EPI_SWIGLU) {
+                const int hid = t.n0 + (ent & 127);
+                n = hid < F ? (ent < 128 ? hid : F + hid) : N;
+            } else {
+                n = t.n0 + ent;
+            }
+            const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(g.w_scale + (int64_t)t.e * N), (short)0, N * 4, kBufDword3);
+            dma_b32(sres, n < N ? (uint32_t)n * 4u : kOOR, (uint32_t)(uintptr_t)(lds_t*)&wsbuf[buf][64 * wave]);
+            uint32_t aoff;
+            if constexpr (GATHER) {
+                const uint32_t tok = (uint32_t)tokbuf[buf][ent];
+                aoff = ent < t.rows && tok < (uint32_t)g.a_rows ? tok * 4u : kOOR;
+            } else {
+                aoff = ent < t.rows ? (uint32_t)ent * 4u : kOOR;
+            }
+            // (base and size read from lane 0: the compiler cannot otherwise
+            // tell that they are uniform, and the load needs them in scalar
+            // registers)
+            const uint64_t ab = (uint64_t)(uintptr_t)(g.a_scale + (GATHER ? 0 : t.s0));
+            const int alo = __builtin_amdgcn_readfirstlane((int)(uint32_t)ab);
+            const int ahi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(ab >> 32));
+            const int abytes = __builtin_amdgcn_readfirstlane(GATHER ? (int)(g.a_rows * 4) : t.rows * 4);
+            const __amdgpu_buffer_rsrc_t rres = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(uintptr_t)(((uint64_t)(uint32_t)ahi << 32) | (uint32_t)alo), (short)0, abytes, kBufDword3);
+            dma_b32(rres, aoff, (uint32_t)(uintptr_t)(lds_t*)&asbuf[buf][64 * wave]);
+        }
+    };
     // z is 0; a laundered z (opaque to the compiler) makes it compute the
     // offsets again instead of keeping an earlier copy in registers.
     auto setup_b = [&](const Tile& t, Offsets& o, uint32_t z, int buf) {
+        if constexpr (GATHER && !FP8) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int R = 64 * wave + 8 * i + (lane >> 3);
-            const uint32_t seg = (uint32_t)segk[i & 1] * 2u + z;
-            if constexpr (GATHER) {
+            for (int i = 0; i < 8; ++i) {
+                const int R = 64 * wave + 8 * i + (lane >> 3);
+                const uint32_t seg = (uint32_t)segk[i & 1] * ES + z;
                 const uint32_t tok = (uint32_t)tokbuf[buf][min(R, t.rows - 1)];
-                o.a[i] = tok < (uint32_t)g.a_rows ? tok * (uint32_t)K * 2u + seg : kOOR;
-            } else {
-                o.a[i] = (uint32_t)min(R, t.rows - 1) * (uint32_t)K * 2u + seg;
+                o.a[i] = tok < (uint32_t)g.a_rows ? tok * ((uint32_t)K * ES) + seg : kOOR;
             }
-            if constexpr (EPI == EPI_SWIGLU) {
-                // tile row R -> wave column half R / 128, MFMA tile (R / 32) % 4
-                // (0, 1: gate; 2, 3: up), so a wave's gate and up accumulators
-                // of one hidden unit sit in the same lane and register
-                const int tt = (R >> 5) & 3;
-                const int hid = t.n0 + (R >> 7) * 64 + (tt & 1) * 32 + (R & 31);
-                o.b[i] = hid < F ? (uint32_t)(tt >= 2 ? F + hid : hid) * (uint32_t)K * 2u + seg : kOOR;
-            } else {
-                const int n = t.n0 + R;
-                o.b[i] = n < N ? (uint32_t)n * (uint32_t)K * 2u + seg : kOOR;
-            }
+        }
+    };
+    // Byte offset of the lane's segment in load row i of A (slot-major) or W:
+    // computed at each load from the tile's scalars (registers are scarce in
+    // the K loop).
+    // (fp8 gather reads the token from the tile's LDS copy at each load: the
+    // fp8 kernels have no registers to spare for the offsets)
+    auto a_off = [&](const Tile& t, const Offsets& o, int i, int tb) -> uint32_t {
+        const int R = 64 * wave + 8 * i + (lane >> 3);
+        if constexpr (GATHER && FP8) {
+            const uint32_t tok = (uint32_t)tokbuf[tb][min(R, t.rows - 1)];
+            return tok < (uint32_t)g.a_rows ? tok * ((uint32_t)K * ES) + (uint32_t)segk[i & 1] * ES : kOOR;
+        } else if constexpr (GATHER) {
+            return o.a[i];
+        } else {
+            return (uint32_t)min(R, t.rows - 1) * ((uint32_t)K * ES) + (uint32_t)segk[i & 1] * ES;
+        }
+    };
+    auto b_off = [&](const Tile& t, int i) -> uint32_t {
+        const int R = 64 * wave + 8 * i + (lane >> 3);
+        const uint32_t seg = (uint32_t)segk[i & 1] * ES;
+        if constexpr (EPI == EPI_SWIGLU) {
+            // tile row R -> wave column half R / 128, MFMA tile (R / 32) % 4
+            // (0, 1: gate; 2, 3: up), so a wave's gate and up accumulators
+            // of one hidden unit sit in the same lane and register
+            const int tt = (R >> 5) & 3;
+            const int hid = t.n0 + (R >> 7) * 64 + (tt & 1) * 32 + (R & 31);
+            return hid < F ? (uint32_t)(tt >= 2 ? F + hid : hid) * ((uint32_t)K * ES) + seg : kOOR;
+        } else {
+            const int n = t.n0 + R;
+            return n < N ? (uint32_t)n * ((uint32_t)K * ES) + seg : kOOR;
         }
     };
 
@@ -303,14 +380,14 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // One direct load of a tile's chunk c: q even -> A block q / 2, q odd -> W
     // block q / 2.  A chunk that runs past K masks the segments at or past K
     // (K is a multiple of 8, so a segment is all in or all out).
-    auto dma_one = [&](const Tile& t, const Offsets& o, int c, int par, int q) {
+    auto dma_one = [&](const Tile& t, const Offsets& o, int tb, int c, int par, int q) {
         const int i = q >> 1;
         const uint32_t sb =
             lds0 + (uint32_t)((c + par) & 1) * kStage + (uint32_t)wave * 8192u + (uint32_t)i * 1024u;
         const uint32_t soff = (uint32_t)c * 128u;
-        const uint32_t kmask = (c + 1) * kKC <= K || c * kKC + segk[i & 1] < K ? 0u : kOOR;
-        if (q & 1) dma_b128(t.wres, o.b[i] | kmask, soff, sb + kHalf);
-        else dma_b128(t.ares, o.a[i] | kmask, soff, sb);
+        const uint32_t kmask = (c + 1) * KC <= K || c * KC + segk[i & 1] < K ? 0u : kOOR;
+        if (q & 1) dma_b128(t.wres, b_off(t, i) | kmask, soff, sb + kHalf);
+        else dma_b128(t.ares, a_off(t, o, i, tb) | kmask, soff, sb);
     };
 
     f32x16_t acc[4][4];
@@ -326,19 +403,42 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int flane = ((lane & 31) >> 3) * 1024 + (lane & 7) * 128;
     const unsigned char* const abase = smem + wm * 16384 + flane;
     const unsigned char* const bbase = smem + kHalf + wn * 16384 + flane;
-    u32x4_t f[4][2][4];       // [k-step][A, W][tile]: a whole chunk's fragments
-    // fragment q of k-step ks of the chunk in stage st (q < 4: A tile q, else
-    // W tile q - 4)
-    auto frag_one = [&](int st, int ks, int q) {
-        const int off = st * kStage + (((2 * ks + (lane >> 5)) ^ fkey) << 4) + (q & 3) * 4096;
-        f[ks][q >> 2][q & 3] = *reinterpret_cast<const u32x4_t*>((q < 4 ? abase : bbase) + off);
+    // A whole chunk's fragments, [k-step][A, W][tile]: 16 bytes per lane
+    // (bf16) or 32 (fp8, filled by two reads).
+    using Frag = std::conditional_t<FP8, u32x8_t, u32x4_t>;
+    Frag f[NKS][2][4];
+    // Read r of k-step ks of the chunk in stage st, r < RPK: fragment q = r
+    // (bf16) or r / 2 (fp8, piece r % 2); q < 4: A tile q, else W tile q - 4.
+    // Lane l reads row R = 32 (q % 4) + l % 32, 16-byte segment 2 ks + l / 32
+    // (bf16) or 4 ks + 2 (l / 32) + piece (fp8).
+    constexpr int RPK = FP8 ? 16 : 8;
+    auto read_r = [&](int st, int ks, int r) {
+        const int q = FP8 ? r >> 1 : r;
+        const int sgi = FP8 ? 4 * ks + 2 * (lane >> 5) + (r & 1) : 2 * ks + (lane >> 5);
+        const int off = st * kStage + ((sgi ^ fkey) << 4) + (q & 3) * 4096;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((q < 4 ? abase : bbase) + off);
+        if constexpr (FP8) {
+            Frag& fr = f[ks][q >> 2][q & 3];
+            const int h = 4 * (r & 1);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) fr[h + w] = v[w];
+        } else {
+            f[ks][q >> 2][q & 3] = v;
+        }
     };
     // MFMA m of k-step ks: slot tile m / 4, feature tile m % 4
     auto mfma_one = [&](int ks, int m) {
         const int i = m >> 2, j = m & 3;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
-                                                            __builtin_bit_cast(bf16x8_t, f[ks][0][i]), acc[i][j],
-                                                            0, 0, 0);
+        if constexpr (FP8) {
+            // formats 0, 0: fp8 e4m3 both; block scales 127: 2^0
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                __builtin_bit_cast(i32x8_t, f[ks][1][j]), __builtin_bit_cast(i32x8_t, f[ks][0][i]), acc[i][j], 0, 0,
+                0, 127, 0, 127);
+        } else {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
+                                                                __builtin_bit_cast(bf16x8_t, f[ks][0][i]),
+                                                                acc[i][j], 0, 0, 0);
+        }
     };
     auto pin = [&]() { __builtin_amdgcn_sched_barrier(0); };
     auto barrier = [&]() {
@@ -355,21 +455,22 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     if (!cur.valid) return;
     if (GATHER) dma_wait_barrier<0>();
     setup_b(cur, co, 0u, buf);
+    setup_scales(cur, buf);   // (older than the chunk loads below: their wait covers it)
     int par = 0;              // stage of chunk c: (c + par) & 1
     // First tile: chunks 0 and 1 in flight, wait for chunk 0, read its
     // k-steps 0..2.  Later tiles find theirs prefetched (below).
     {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) dma_one(cur, co, 0, par, q);
+        for (int q = 0; q < 16; ++q) dma_one(cur, co, buf, 0, par, q);
         if (nk > 1) {
 #pragma unroll
-            for (int q = 0; q < 16; ++q) dma_one(cur, co, 1, par, q);
+            for (int q = 0; q < 16; ++q) dma_one(cur, co, buf, 1, par, q);
             dma_wait_barrier<16>();
         } else {
             dma_wait_barrier<0>();
         }
 #pragma unroll
-        for (int q = 0; q < 24; ++q) frag_one(par & 1, q >> 3, q & 7);
+        for (int r = 0; r < (NKS - 1) * RPK; ++r) read_r(par & 1, r / RPK, r % RPK);
     }
     // With two chunks or more per tile, the last two chunks of a tile load the
     // next tile's chunks 0 and 1, so a tile starts with its data in LDS and the
@@ -387,39 +488,77 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // pipe keeps a queued MFMA while they issue.
     auto step = [&](int c, auto load, bool more2, bool more1) {
         const int st = (c + par) & 1;
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            mfma_one(0, m);
-            pin();
-            if (m < 8) frag_one(st, 3, m);
-            pin();
-        }
-        // (the builtin, not inline assembly: the compiler then knows these
-        // reads are complete and adds no waits for them later)
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-        barrier();
-#pragma unroll
-        for (int m = 0; m < 32; ++m) {
-            mfma_one(1 + (m >> 4), m & 15);
-            pin();
-            if (more2 && (m & 1)) load(m >> 1);
-            pin();
-        }
-        if (more1) {
-            if (more2) dma_wait_barrier<16>();
-            else dma_wait_barrier<0>();
-        }
         const int st1 = st ^ 1;                    // the stream's next chunk
         const bool rd1 = c + 1 < nk;
+        if constexpr (!FP8) {
 #pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            mfma_one(3, m);
-            pin();
-            if (rd1) {
-                const int r0 = (3 * m) / 2, r1 = (3 * m + 3) / 2;   // 24 reads over 16 MFMAs
-                for (int r = r0; r < r1; ++r) frag_one(st1, r >> 3, r & 7);
+            for (int m = 0; m < 16; ++m) {
+                mfma_one(0, m);
+                pin();
+                if (m < 8) read_r(st, 3, m);
+                pin();
             }
-            pin();
+            // (the builtin, not inline assembly: the compiler then knows these
+            // reads are complete and adds no waits for them later)
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            barrier();
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                mfma_one(1 + (m >> 4), m & 15);
+                pin();
+                if (more2 && (m & 1)) load(m >> 1);
+                pin();
+            }
+            if (more1) {
+                if (more2) dma_wait_barrier<16>();
+                else dma_wait_barrier<0>();
+            }
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                mfma_one(3, m);
+                pin();
+                if (rd1) {
+                    const int r0 = (3 * m) / 2, r1 = (3 * m + 3) / 2;   // 24 reads over 16 MFMAs
+                    for (int r = r0; r < r1; ++r) read_r(st1, r >> 3, r & 7);
+                }
+                pin();
+            }
+        } else {
+            // Two k-steps of 16 MFMAs (each twice a bf16 MFMA's time), in the
+            // same proportions: the last k-step's 16 reads under the first 8
+            // MFMAs, the loads under the next 16, the next chunk's k-step 0
+            // under the last 8.
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                mfma_one(0, m);
+                pin();
+                read_r(st, 1, 2 * m);
+                read_r(st, 1, 2 * m + 1);
+                pin();
+            }
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            barrier();
+#pragma unroll
+            for (int m = 8; m < 24; ++m) {
+                mfma_one(m >> 4, m & 15);
+                pin();
+                if (more2) load(m - 8);
+                pin();
+            }
+            if (more1) {
+                if (more2) dma_wait_barrier<16>();
+                else dma_wait_barrier<0>();
+            }
+#pragma unroll
+            for (int m = 8; m < 16; ++m) {
+                mfma_one(1, m);
+                pin();
+                if (rd1) {
+                    read_r(st1, 0, 2 * (m - 8));
+                    read_r(st1, 0, 2 * (m - 8) + 1);
+                }
+                pin();
+            }
         }
     };
 
@@ -430,18 +569,22 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         // chunks whose stream successor two ahead is this tile's own
         const int nmain = nk - 2;
         for (int c = 0; c < nmain; ++c)
-            step(c, [&](int q) { dma_one(cur, co, c + 2, par, q); }, true, true);
+            step(c, [&](int q) { dma_one(cur, co, buf, c + 2, par, q); }, true, true);
         // the last two chunks: the stream's chunks two ahead are the next
         // tile's 0 and 1
         // (the next tile's tokens: its token load is older than the stream's
         // last 16 loads, so any chunk wait of the loop above covered it; with
         // no such wait, wait here)
+        // (fp8: the next tile's scales, now that every wave has met the others
+        // after the last epilogue -- in the loop above or just here -- and
+        // before the next tile's chunk loads, whose waits cover them)
         if (more_tiles) {
-            if (GATHER && nmain <= 0) dma_wait_barrier<0>();
+            if ((GATHER || FP8) && nmain <= 0) dma_wait_barrier<0>();
             setup_b(nxt, no, 0u, buf ^ 1);
+            setup_scales(nxt, buf ^ 1);
         }
         for (int c = max(nmain, 0); c < nk; ++c)
-            step(c, [&](int q) { dma_one(nxt, no, c + 2 - nk, par + nk, q); }, more_tiles,
+            step(c, [&](int q) { dma_one(nxt, no, buf ^ 1, c + 2 - nk, par + nk, q); }, more_tiles,
                  c + 1 < nk || more_tiles);
 
         // Epilogue straight from the accumulators: lane l holds slot (wm * 4 +
@@ -458,12 +601,55 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
+        // fp8: the scale of slot tile i's row of a, and the weight-row scales
+        // of 4 consecutive output columns, from the tile's copies in LDS
+        // (wsbuf entry = output column of the tile; SwiGLU: gate column, or
+        // 128 + its up column)
+        auto a_row_scale = [&](int i) -> float { return asbuf[buf][(wm * 4 + i) * 32 + r32]; };
+        auto w_scales = [&](int col) -> float4 { return *reinterpret_cast<const float4*>(&wsbuf[buf][col]); };
         if constexpr (EPI == EPI_SWIGLU) {
             // h = (g * sigmoid(g)) * u in binary32, from the gate tiles j = 0, 1
             // and the up tiles j + 2 of the same lane and register; 128 hidden
             // columns per tile, wave column half wn holds hidden wn * 64 ...
             const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(
                 g.c + cur.s0 * F, (short)0, cur.rows * F * 2, kBufDword3);
+            if constexpr (FP8) {
+                float sa[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sa[i] = a_row_scale(i);
+                // hidden tile outermost: its gate and up weight-row scales are
+                // loaded once
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    float4 wg[4], wu[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int col = wn * 64 + j * 32 + 8 * r + 4 * kh;
+                        wg[r] = w_scales(col);
+                        wu[r] = w_scales(128 + col);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = (wm * 4 + i) * 32 + r32;
+                        u32x2_t P[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            __builtin_amdgcn_sched_barrier(0);   // one 4-value group at a time
+                            float h[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const float gv = (acc[i][j][4 * r + e] * sa[i]) * wg[r][e];
+                                const float uv = (acc[i][j + 2][4 * r + e] * sa[i]) * wu[r][e];
+                                h[e] = (gv * sigmoid(gv)) * uv;
+                            }
+                            P[r] = u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                        }
+                        store_row_segment(P, cres, row < cur.rows, (uint32_t)row * (uint32_t)F,
+                                          cur.n0 + wn * 64 + j * 32, F, kh);
+                    }
+                }
+            } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 __builtin_amdgcn_sched_barrier(0);       // one slot tile at a time: few temporaries
@@ -486,6 +672,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                                       cur.n0 + wn * 64 + j * 32, F, kh);
                 }
             }
+            }
         } else {
             const __amdgpu_buffer_rsrc_t cres = __builtin_amdgcn_make_buffer_rsrc(
                 g.c + cur.s0 * N, (short)0, cur.rows * N * 2, kBufDword3);
@@ -500,7 +687,33 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                     const int row = (wm * 4 + i) * 32 + r32;
                     sc[i] = g.row_scale[cur.s0 + min(row, cur.rows - 1)];
                 }
+                if constexpr (FP8) sc[i] = a_row_scale(i);
             }
+            if constexpr (FP8) {
+                // feature tile outermost: its 16 weight-row scales are loaded once
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    float4 ws[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ws[r] = w_scales((wn * 4 + j) * 32 + 8 * r + 4 * kh);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        __builtin_amdgcn_sched_barrier(0);   // one 32 x 32 tile at a time
+                        const int row = (wm * 4 + i) * 32 + r32;
+                        u32x2_t P[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            float v[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = (sc[i] * acc[i][j][4 * r + e]) * ws[r][e];
+                            P[r] = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        }
+                        store_row_segment(P, cres, row < cur.rows, (uint32_t)row * (uint32_t)N,
+                                          cur.n0 + (wn * 4 + j) * 32, N, kh);
+                    }
+                }
+            } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if constexpr (EPI == EPI_ROW_SCALE) __builtin_amdgcn_sched_barrier(0);   // one slot tile at a time
@@ -521,6 +734,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                                       cur.n0 + (wn * 4 + j) * 32, N, kh);
                 }
             }
+            }
         }
         if (!nxt.valid) break;
         // (nothing below moves into the epilogue, where it would hold registers)
@@ -535,14 +749,15 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             // barrier makes that hold for all waves)
             dma_wait_barrier<0>();
             setup_b(nxt, no, 0u, buf ^ 1);
+            setup_scales(nxt, buf ^ 1);
 #pragma unroll
-            for (int q = 0; q < 16; ++q) dma_one(nxt, no, 0, par + nk, q);
+            for (int q = 0; q < 16; ++q) dma_one(nxt, no, buf ^ 1, 0, par + nk, q);
             dma_wait_barrier<0>();
         }
         // the next tile's chunk 0 is in its stage for every wave (the last
         // step's wait and barrier, or the one just above): its k-steps 0..2
 #pragma unroll
-        for (int q = 0; q < 24; ++q) frag_one((par + nk) & 1, q >> 3, q & 7);
+        for (int r = 0; r < (NKS - 1) * RPK; ++r) read_r((par + nk) & 1, r / RPK, r % RPK);
         par = (par + nk) & 1;
         cur = nxt;
         buf ^= 1;
@@ -575,33 +790,44 @@ int num_cus()
 
 using namespace et;
 
-extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
-                              const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
-                              int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream)
+namespace {
+
+// Argument checks and launch of both entry points (es = bytes per operand
+// element: 2 for bf16, 1 for fp8).
+int launch_expert_gemm(const char* fn, int es, const void* a, int64_t a_rows, const float* a_scale,
+                       const int32_t* sorted_token, const void* w, const float* w_scale,
+                       const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
+                       int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream)
 {
-    const char* fn = "et_expert_gemm";
     const int64_t E = num_experts;
+    const bool fp8 = es == 1;
     if (E < 1 || E > ET_MAX_EXPERTS)
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": num_experts must be in [1, " +
                                                  std::to_string(ET_MAX_EXPERTS) + "]");
-    if (K < 8 || K % 8 != 0 || K >= (int64_t(1) << 22))
-        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": K must be a positive multiple of 8 below 2^22");
+    const int64_t kq = 16 / es;   // k per 16-byte segment
+    if (K < kq || K % kq != 0 || K >= (int64_t(1) << 22))
+        return fail(ET_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": K must be a positive multiple of " + std::to_string(kq) + " below 2^22");
     if (N < 8 || N % 8 != 0)
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N must be a positive multiple of 8");
     if (epilogue != ET_GEMM_PLAIN && epilogue != ET_GEMM_ROW_SCALE && epilogue != ET_GEMM_SWIGLU)
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": unknown epilogue " + std::to_string(epilogue));
+    if (fp8 && epilogue == ET_GEMM_ROW_SCALE)
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": the fp8 GEMM has the plain and SwiGLU epilogues");
     if (epilogue == ET_GEMM_SWIGLU && N % 16 != 0)
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": SwiGLU needs N = 2 F with F a multiple of 8");
-    if (N * K * 2 >= (int64_t(1) << 31))
-        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": one expert's weight (N * K * 2 bytes) must be below 2 GiB");
+    if (N * K * es >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": one expert's weight (N * K * element bytes) must be below 2 GiB");
     if (kBM * N * 2 >= (int64_t(1) << 31))
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": N too large");
     if (slot_capacity < 0 || slot_capacity >= (int64_t(1) << 31))
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": slot_capacity out of range");
     const bool gather = sorted_token != nullptr;
-    if (gather && (a_rows < 0 || a_rows * K * 2 >= (int64_t(1) << 31)))
-        return fail(ET_ERR_INVALID_ARGUMENT,
-                    std::string(fn) + ": in gather mode the token rows (a_rows * K * 2 bytes) must be below 2 GiB");
+    if (gather && (a_rows < 0 || a_rows * K * es >= (int64_t(1) << 31)))
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) +
+                                                 ": in gather mode the token rows (a_rows * K * element bytes) must "
+                                                 "be below 2 GiB");
     if (slot_capacity == 0) return ET_OK;
     if (!a || !w || !expert_offsets || !c) return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": null pointer");
     if (epilogue == ET_GEMM_ROW_SCALE && !row_scale)
@@ -609,6 +835,10 @@ extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sort
     if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15) ||
         (reinterpret_cast<uintptr_t>(c) & 15))
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": a, w and c must be 16-byte aligned");
+    if (fp8 && (!a_scale || !w_scale || (reinterpret_cast<uintptr_t>(w_scale) & 15) ||
+                (reinterpret_cast<uintptr_t>(a_scale) & 3)))
+        return fail(ET_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": a_scale (4-byte aligned) and w_scale (16-byte aligned) are required");
     const int64_t nN = epilogue == ET_GEMM_SWIGLU ? (N / 2 + kBN / 2 - 1) / (kBN / 2) : (N + kBN - 1) / kBN;
     const int64_t qmax = ((slot_capacity + kBM - 1) / kBM + E) * nN;
     if (qmax >= (int64_t(1) << 31))
@@ -616,19 +846,47 @@ extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sort
     const int64_t blocks = std::min<int64_t>((int64_t)num_cus(), qmax);
     const dim3 grid((unsigned)(8 * ((blocks + 7) / 8)));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const GemmArgs args{static_cast<const uint16_t*>(a), sorted_token, static_cast<const uint16_t*>(w),
-                        expert_offsets, static_cast<uint16_t*>(c), row_scale, a_rows, slot_capacity,
-                        (int)K, (int)N, (int)E};
+    const GemmArgs args{static_cast<const unsigned char*>(a), sorted_token, static_cast<const unsigned char*>(w),
+                        expert_offsets, static_cast<uint16_t*>(c), row_scale, a_scale, w_scale, a_rows,
+                        slot_capacity, (int)K, (int)N, (int)E};
     const dim3 block(kThreads);
-    switch (epilogue * 2 + (gather ? 1 : 0)) {
-        case 0: expert_gemm_kernel<false, EPI_PLAIN><<<grid, block, 0, s>>>(args); break;
-        case 1: expert_gemm_kernel<true, EPI_PLAIN><<<grid, block, 0, s>>>(args); break;
-        case 2: expert_gemm_kernel<false, EPI_ROW_SCALE><<<grid, block, 0, s>>>(args); break;
-        case 3: expert_gemm_kernel<true, EPI_ROW_SCALE><<<grid, block, 0, s>>>(args); break;
-        case 4: expert_gemm_kernel<false, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
-        default: expert_gemm_kernel<true, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
+    if (fp8) {
+        switch ((epilogue == ET_GEMM_SWIGLU ? 2 : 0) + (gather ? 1 : 0)) {
+            case 0: expert_gemm_kernel<false, EPI_PLAIN, true><<<grid, block, 0, s>>>(args); break;
+            case 1: expert_gemm_kernel<true, EPI_PLAIN, true><<<grid, block, 0, s>>>(args); break;
+            case 2: expert_gemm_kernel<false, EPI_SWIGLU, true><<<grid, block, 0, s>>>(args); break;
+            default: expert_gemm_kernel<true, EPI_SWIGLU, true><<<grid, block, 0, s>>>(args); break;
+        }
+    } else {
+        switch (epilogue * 2 + (gather ? 1 : 0)) {
+            case 0: expert_gemm_kernel<false, EPI_PLAIN><<<grid, block, 0, s>>>(args); break;
+            case 1: expert_gemm_kernel<true, EPI_PLAIN><<<grid, block, 0, s>>>(args); break;
+            case 2: expert_gemm_kernel<false, EPI_ROW_SCALE><<<grid, block, 0, s>>>(args); break;
+            case 3: expert_gemm_kernel<true, EPI_ROW_SCALE><<<grid, block, 0, s>>>(args); break;
+            case 4: expert_gemm_kernel<false, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
+            default: expert_gemm_kernel<true, EPI_SWIGLU><<<grid, block, 0, s>>>(args); break;
+        }
     }
     return check_launch("expert_gemm_kernel");
+}
+
+}  // namespace
+
+extern "C" int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, const void* w,
+                              const int32_t* expert_offsets, int64_t num_experts, int64_t K, int64_t N,
+                              int64_t slot_capacity, int epilogue, const float* row_scale, void* c, void* stream)
+{
+    return launch_expert_gemm("et_expert_gemm", 2, a, a_rows, nullptr, sorted_token, w, nullptr, expert_offsets,
+                              num_experts, K, N, slot_capacity, epilogue, row_scale, c, stream);
+}
+
+extern "C" int et_expert_gemm_fp8(const void* a, int64_t a_rows, const float* a_scale, const int32_t* sorted_token,
+                                  const void* w, const float* w_scale, const int32_t* expert_offsets,
+                                  int64_t num_experts, int64_t K, int64_t N, int64_t slot_capacity, int epilogue,
+                                  void* c, void* stream)
+{
+    return launch_expert_gemm("et_expert_gemm_fp8", 1, a, a_rows, a_scale, sorted_token, w, w_scale, expert_offsets,
+                              num_experts, K, N, slot_capacity, epilogue, nullptr, c, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -415,6 +415,45 @@ def expert_gemm(a: torch.Tensor, w: torch.Tensor, plan: RoutingPlan, *, gather: 
     return c
 
 
+def expert_gemm_fp8(a: torch.Tensor, a_scale: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor,
+                    plan: RoutingPlan, *, gather: bool = True, epilogue: str = "none",
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The expert grouped GEMM on fp8 e4m3 operands (``torch.float8_e4m3fn``):
+    c[s] = ((A[row(s)] @ W[e(s)]^T) * a_scale[row(s)]) * w_scale[e(s)], bf16
+    [rows, N] (or [rows, N / 2] with ``epilogue="swiglu"``).  a [T or rows, K],
+    a_scale f32 [a rows], w [E, N, K], w_scale f32 [E, N]; row(s) as in
+    :func:`expert_gemm`.  K a multiple of 16."""
+    if a.dtype != torch.float8_e4m3fn or w.dtype != torch.float8_e4m3fn:
+        raise TypeError("a and w must be torch.float8_e4m3fn")
+    dev = a.device
+    _require_device(a, "a")
+    if a.dim() != 2 or not a.is_contiguous():
+        raise ValueError("a must be a contiguous 2-D tensor")
+    if w.dim() != 3 or not w.is_contiguous() or w.device != dev:
+        raise ValueError("w must be a contiguous [E, N, K] tensor on a's device")
+    _check_plan(plan, dev)
+    E, N, K = w.shape
+    if E != plan.num_experts or a.shape[1] != K:
+        raise ValueError(f"w must be [{plan.num_experts}, N, {a.shape[1]}]")
+    _require(a_scale, "a_scale", torch.float32, 1, dev)
+    _require(w_scale, "w_scale", torch.float32, 2, dev)
+    if a_scale.shape[0] != a.shape[0] or tuple(w_scale.shape) != (E, N):
+        raise ValueError("a_scale must be [a rows] and w_scale [E, N]")
+    epi = {"none": ET_GEMM_PLAIN, "swiglu": ET_GEMM_SWIGLU}.get(epilogue)
+    if epi is None:
+        raise ValueError(f"unknown epilogue {epilogue!r} (the fp8 GEMM has 'none' and 'swiglu')")
+    if not gather and a.shape[0] != plan.rows:
+        raise ValueError(f"slot-major a must have {plan.rows} rows")
+    ncol = N // 2 if epi == ET_GEMM_SWIGLU else N
+    c = _out_or_new(out, (plan.rows, ncol), torch.bfloat16, dev, "out")
+    with torch.cuda.device(dev):
+        rc = lib().et_expert_gemm_fp8(_vp(a), a.shape[0], _vp(a_scale), _vp(plan.sorted_token) if gather else None,
+                                      _vp(w), _vp(w_scale), _vp(plan.expert_offsets), E, K, N, plan.rows, epi,
+                                      _vp(c), _stream(dev))
+    check("et_expert_gemm_fp8", rc)
+    return c
+
+
 def expert_weight_transpose(w: torch.Tensor, plan: RoutingPlan, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """wt[e] = w[e]^T ([E, K, N] bf16) for the plan's experts with slots (the
     other experts' blocks of ``out`` are left as they were)."""

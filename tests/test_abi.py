@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 23
+    assert len(syms) == 24
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name
@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 6" in hdr
-    assert et.lib().et_abi_version() == 6
+    assert "#define ET_ABI_VERSION 7" in hdr
+    assert et.lib().et_abi_version() == 7
 
 
 def test_workspace_sizes(et):
@@ -184,3 +184,20 @@ def test_swiglu_rejects_bad_arguments(et):
     # no slot rows: nothing to do, nothing launched
     assert lib.et_swiglu_fwd(p, 16, p, 4, 0, p, None) == 0
     assert lib.et_swiglu_bwd(p, p, 16, p, 4, 0, p, None) == 0
+
+
+def test_expert_gemm_fp8_rejects_bad_arguments(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    # (a, a_rows, a_scale, sorted_token, w, w_scale, expert_offsets, E, K, N, slot_capacity, epilogue, c, stream)
+    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, p, p, 4, 72, 64, 16, 0, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "multiple of 16" in _err(et)
+    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, p, p, 4, 64, 64, 16, 1, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "plain and SwiGLU" in _err(et)
+    assert lib.et_expert_gemm_fp8(p, 16, None, p, p, p, p, 4, 64, 64, 16, 0, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "a_scale" in _err(et)
+    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, ctypes.c_void_p(0x1004), p, 4, 64, 64, 16, 0, p, None) \
+        == ET_ERR_INVALID_ARGUMENT
+    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, p, p, 4, 64, 24, 16, 2, p, None) == ET_ERR_INVALID_ARGUMENT
+    assert "SwiGLU" in _err(et)
+    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, p, p, 4, 64, 64, 0, 0, p, None) == 0   # nothing to do
