@@ -12,8 +12,8 @@ backward (dispatch backward with the router input gradient, router weight
 gradient) are measured separately after the timed steps and reported in
 "router_producer" and "router_backward"; so is the expert grouped GEMM that
 consumes the dispatch ("expert_gemm": the gate/up projection with the dispatch
-fused into its operand load, the down projection, and torch's grouped GEMM on
-the same shapes).
+fused into its operand load, also on fp8 e4m3 operands, the down projection,
+the backward, and torch's grouped GEMM on the same shapes).
 Yp and dXp are separate resident buffers standing in for the expert FFN's
 output and input-gradient (the FFN itself is not part of the path).
 
@@ -243,6 +243,7 @@ def router_backward(et, dev, stream, plan, X, DXP, DGATE, DL, reps: int = 10) ->
 
 EXPERT_FFN = 1536          # expert FFN width of the gate/up and down projections (Qwen3-MoE's, d = 4096, E = 128)
 MFMA_BF16_PEAK = 2.5e15   # MI355X dense bf16 matrix peak, FLOP/s
+MFMA_FP8_PEAK = 5.0e15    # MI355X dense fp8 matrix peak, FLOP/s
 
 
 def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
@@ -285,6 +286,26 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     hs = torch.empty(S, F, dtype=torch.bfloat16, device=dev)
     t_up_swiglu = timed(lambda: et.expert_gemm(X, w1, plan, epilogue="swiglu", out=hs))
     del hs
+    # the same projection on fp8 e4m3 operands, each row of X and of the
+    # weight scaled by its amax / 448 (the binary32 scales are applied in the
+    # epilogue); its distance from the bf16 product is the quantization's
+    xsc = X.float().abs().amax(1).clamp_min(1e-30) / 448.0
+    xq = (X.float() / xsc[:, None]).to(torch.float8_e4m3fn)
+    w1sc = torch.empty(E, 2 * F, dtype=torch.float32, device=dev)
+    w1q = torch.empty(E, 2 * F, d, dtype=torch.float8_e4m3fn, device=dev)
+    for e in range(E):
+        we = w1[e].float()
+        w1sc[e] = we.abs().amax(1).clamp_min(1e-30) / 448.0
+        w1q[e] = (we / w1sc[e][:, None]).to(torch.float8_e4m3fn)
+        del we
+    h8 = torch.empty(S, 2 * F, dtype=torch.bfloat16, device=dev)
+    t_up8 = timed(lambda: et.expert_gemm_fp8(xq, xsc, w1q, w1sc, plan, out=h8))
+    hs8 = torch.empty(S, F, dtype=torch.bfloat16, device=dev)
+    t_up8_swiglu = timed(lambda: et.expert_gemm_fp8(xq, xsc, w1q, w1sc, plan, epilogue="swiglu", out=hs8))
+    torch.cuda.synchronize()
+    nr = min(S, 65536)
+    rel8 = ((h8[:nr].float() - h[:nr].float()).norm() / h[:nr].float().norm()).item()
+    del xq, xsc, w1q, w1sc, h8, hs8
     t_down = timed(lambda: et.expert_gemm(a2, w2, plan, gather=False, out=y))
     t_disp = timed(lambda: et.dispatch(X, plan, out=xp))
     w1t, w2t = w1.transpose(1, 2), w2.transpose(1, 2)
@@ -334,6 +355,11 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
                         "torch_grouped_mm_ms": round(t_up_lib, 3), "dispatch_ms": round(t_disp, 3),
                         "torch_dispatch_plus_grouped_mm_ms": round(t_disp + t_up_lib, 3),
                         "swiglu_epilogue_ms": round(t_up_swiglu, 3)},
+            "gate_up_fp8": {"K": d, "N": 2 * F, "mode": "gather (dispatch fused)", "operands": "e4m3, row scales",
+                            "ms": round(t_up8, 3), "TFLOP/s": round(fl_up / (t_up8 * 1e-3) / 1e12, 1),
+                            "frac": round(fl_up / (t_up8 * 1e-3) / MFMA_FP8_PEAK, 4),
+                            "swiglu_epilogue_ms": round(t_up8_swiglu, 3),
+                            "relative_error_vs_bf16": round(rel8, 4)},
             "down": {"K": F, "N": d, "mode": "slot-major", "ms": round(t_down, 3),
                      "TFLOP/s": round(fl_down / (t_down * 1e-3) / 1e12, 1),
                      "frac": round(fl_down / (t_down * 1e-3) / MFMA_BF16_PEAK, 4),
@@ -556,6 +582,10 @@ def main() -> int:
               f"epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} ms + dispatch "
               f"{gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; torch grouped "
               f"{dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
+        g8 = eg["gate_up_fp8"]
+        print(f"  expert GEMM fp8: gate/up {g8['ms']:.3f} ms ({g8['TFLOP/s']:.0f} TFLOP/s, {100 * g8['frac']:.1f}% of the "
+              f"fp8 peak; with the SwiGLU epilogue {g8['swiglu_epilogue_ms']:.3f} ms; relative error against bf16 "
+              f"{g8['relative_error_vs_bf16']:.4f})", file=sys.stderr)
         bw = eg["backward"]
         print(f"  expert GEMM backward: down dA fused with the combine backward {bw['down_input_grad_fused_combine_bwd_ms']:.3f}"
               f" ms (transpose {bw['weight_transpose_down_ms']:.3f}), gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, "
