@@ -295,8 +295,8 @@ int et_expert_gemm(const void* a, int64_t a_rows, const int32_t* sorted_token, c
  * [a_rows] f32 scales each row of a (a token in gather mode), w_scale [E, N]
  * f32 each weight row.  epilogue: ET_GEMM_PLAIN or ET_GEMM_SWIGLU (h =
  * (g * sigmoid(g)) * u of the scaled gate and up values).  K a multiple of 16
- * below 2^22, N a multiple of 8 (16 for SwiGLU), N*K below 2^31; a, w, c and
- * w_scale 16-byte aligned, a_scale 4-byte aligned.  Integer-valued operands
+ * below 2^22, N a multiple of 8 (16 for SwiGLU), N*K below 2^31; a, w and c
+ * 16-byte aligned, a_scale and w_scale 4-byte aligned.  Integer-valued operands
  * with power-of-two scales and partial sums below 2^24 give the exact
  * product before the bf16 rounding.  Implements an fp8 form of the expert
  * GEMM that consumes the dispatch (no reference counterpart).

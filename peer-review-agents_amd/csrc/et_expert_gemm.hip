@@ -183,8 +183,10 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
     __shared__ int32_t tokbuf[2][kBM];           // gather: the tokens of a tile's slots, by tile parity
-    __shared__ float wsbuf[2][kBN];              // fp8: the weight-row scales of a tile's columns, by parity
-    __shared__ float asbuf[2][kBM];              // fp8: the scales of a tile's rows of a, by parity
+    // fp8: the weight-row scales of a tile's columns and the scales of its
+    // rows of a, by tile parity (read as float4 in the epilogue)
+    __shared__ __attribute__((aligned(16))) float wsbuf[2][kBN];
+    __shared__ __attribute__((aligned(16))) float asbuf[2][kBM];
 
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -835,10 +837,9 @@ int launch_expert_gemm(const char* fn, int es, const void* a, int64_t a_rows, co
     if ((reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(w) & 15) ||
         (reinterpret_cast<uintptr_t>(c) & 15))
         return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": a, w and c must be 16-byte aligned");
-    if (fp8 && (!a_scale || !w_scale || (reinterpret_cast<uintptr_t>(w_scale) & 15) ||
+    if (fp8 && (!a_scale || !w_scale || (reinterpret_cast<uintptr_t>(w_scale) & 3) ||
                 (reinterpret_cast<uintptr_t>(a_scale) & 3)))
-        return fail(ET_ERR_INVALID_ARGUMENT,
-                    std::string(fn) + ": a_scale (4-byte aligned) and w_scale (16-byte aligned) are required");
+        return fail(ET_ERR_INVALID_ARGUMENT, std::string(fn) + ": a_scale and w_scale (4-byte aligned) are required");
     const int64_t nN = epilogue == ET_GEMM_SWIGLU ? (N / 2 + kBN / 2 - 1) / (kBN / 2) : (N + kBN - 1) / kBN;
     const int64_t qmax = ((slot_capacity + kBM - 1) / kBM + E) * nN;
     if (qmax >= (int64_t(1) << 31))

@@ -196,8 +196,9 @@ def test_expert_gemm_fp8_rejects_bad_arguments(et):
     assert "plain and SwiGLU" in _err(et)
     assert lib.et_expert_gemm_fp8(p, 16, None, p, p, p, p, 4, 64, 64, 16, 0, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "a_scale" in _err(et)
-    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, ctypes.c_void_p(0x1004), p, 4, 64, 64, 16, 0, p, None) \
+    assert lib.et_expert_gemm_fp8(p, 16, p, p, p, ctypes.c_void_p(0x1002), p, 4, 64, 64, 16, 0, p, None) \
         == ET_ERR_INVALID_ARGUMENT
+    assert "w_scale" in _err(et)
     assert lib.et_expert_gemm_fp8(p, 16, p, p, p, p, p, 4, 64, 24, 16, 2, p, None) == ET_ERR_INVALID_ARGUMENT
     assert "SwiGLU" in _err(et)
     assert lib.et_expert_gemm_fp8(p, 16, p, p, p, p, p, 4, 64, 64, 0, 0, p, None) == 0   # nothing to do

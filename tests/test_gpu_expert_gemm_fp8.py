@@ -146,3 +146,24 @@ def test_expert_gemm_fp8_leaves_rows_past_the_slots(et, dev):
     assert bool((out[S:] == 3.0).all())
     ref, _ = _reference(x.float(), sa, w.float(), sw, plan, S, True)
     assert torch.equal(out[:S].view(torch.int16), ref.to(torch.float32).to(torch.bfloat16).view(torch.int16))
+
+
+def test_expert_gemm_fp8_scales_at_any_4_byte_offset(et, dev):
+    """Scales are loaded one dword per lane: views that start 4 bytes into
+    their storage give the same bits as aligned copies."""
+    T, K, N, E = 700, 192, 272, 6
+    plan = _plan(et, dev, T, E, 2, seed=13)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    x = _int_f8((T, K), g, dev)
+    w = _int_f8((E, N, K), g, dev)
+    sa, sw = _pow2((T,), g, dev), _pow2((E, N), g, dev)
+    sa1 = torch.empty(T + 1, device=dev)[1:]
+    sa1.copy_(sa)
+    sw1 = torch.empty(E * N + 1, device=dev)[1:].view(E, N)
+    sw1.copy_(sw)
+    assert sa1.data_ptr() % 16 and sw1.data_ptr() % 16
+    for ep in ("none", "swiglu"):
+        c0 = et.expert_gemm_fp8(x, sa, w, sw, plan, epilogue=ep)
+        c1 = et.expert_gemm_fp8(x, sa1, w, sw1, plan, epilogue=ep)
+        assert torch.equal(c0.view(torch.int16), c1.view(torch.int16))
