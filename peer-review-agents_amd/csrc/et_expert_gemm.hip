@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // z is 0; a laundered z (opaque to the compiler) makes it compute the
     // offsets again instead of keeping an earlier copy in registers.
     auto setup_b = [&](const Tile& t, Offsets& o, uint32_t z, int buf) {
-        if constexpr (GATHER && !FP8) {
+        if constexpr (GATHER) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int R = 64 * wave + 8 * i + (lane >> 3);
@@ -348,14 +348,11 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // Byte offset of the lane's segment in load row i of A (slot-major) or W:
     // computed at each load from the tile's scalars (registers are scarce in
     // the K loop).
-    // (fp8 gather reads the token from the tile's LDS copy at each load: the
-    // fp8 kernels have no registers to spare for the offsets)
+    // (gather mode keeps its 8 offsets in registers: reading the token from
+    // LDS at each load would put an LDS wait before every load)
     auto a_off = [&](const Tile& t, const Offsets& o, int i, int tb) -> uint32_t {
         const int R = 64 * wave + 8 * i + (lane >> 3);
-        if constexpr (GATHER && FP8) {
-            const uint32_t tok = (uint32_t)tokbuf[tb][min(R, t.rows - 1)];
-            return tok < (uint32_t)g.a_rows ? tok * ((uint32_t)K * ES) + (uint32_t)segk[i & 1] * ES : kOOR;
-        } else if constexpr (GATHER) {
+        if constexpr (GATHER) {
             return o.a[i];
         } else {
             return (uint32_t)min(R, t.rows - 1) * ((uint32_t)K * ES) + (uint32_t)segk[i & 1] * ES;
