@@ -307,6 +307,18 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
     rel8 = ((h8[:nr].float() - h[:nr].float()).norm() / h[:nr].float().norm()).item()
     del xq, xsc, w1q, w1sc, h8, hs8
     t_down = timed(lambda: et.expert_gemm(a2, w2, plan, gather=False, out=y))
+    # the down projection on fp8 operands (slot-major: one scale per slot row)
+    a2sc = a2.float().abs().amax(1).clamp_min(1e-30) / 448.0
+    a2q = (a2.float() / a2sc[:, None]).to(torch.float8_e4m3fn)
+    w2f = w2.float()
+    w2sc = w2f.abs().amax(2).clamp_min(1e-30) / 448.0
+    w2q = (w2f / w2sc[:, :, None]).to(torch.float8_e4m3fn)
+    del w2f
+    y8 = torch.empty_like(y)
+    t_down8 = timed(lambda: et.expert_gemm_fp8(a2q, a2sc, w2q, w2sc, plan, gather=False, out=y8))
+    torch.cuda.synchronize()
+    rel8_down = ((y8[:nr].float() - y[:nr].float()).norm() / y[:nr].float().norm()).item()
+    del a2q, a2sc, w2q, w2sc, y8
     t_disp = timed(lambda: et.dispatch(X, plan, out=xp))
     w1t, w2t = w1.transpose(1, 2), w2.transpose(1, 2)
     t_up_lib = timed(lambda: torch._grouped_mm(xp, w1t, offs=offs))
@@ -364,6 +376,10 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
                      "TFLOP/s": round(fl_down / (t_down * 1e-3) / 1e12, 1),
                      "frac": round(fl_down / (t_down * 1e-3) / MFMA_BF16_PEAK, 4),
                      "torch_grouped_mm_ms": round(t_down_lib, 3)},
+            "down_fp8": {"K": F, "N": d, "mode": "slot-major", "operands": "e4m3, row scales",
+                         "ms": round(t_down8, 3), "TFLOP/s": round(fl_down / (t_down8 * 1e-3) / 1e12, 1),
+                         "frac": round(fl_down / (t_down8 * 1e-3) / MFMA_FP8_PEAK, 4),
+                         "relative_error_vs_bf16": round(rel8_down, 4)},
             "backward": {"weight_transpose_down_ms": round(t_tr2, 3),
                          "down_input_grad_fused_combine_bwd_ms": round(t_down_bwd, 3),
                          "gate_up_input_grad_ms": round(t_up_bwd, 3),
@@ -585,7 +601,8 @@ def main() -> int:
         g8 = eg["gate_up_fp8"]
         print(f"  expert GEMM fp8: gate/up {g8['ms']:.3f} ms ({g8['TFLOP/s']:.0f} TFLOP/s, {100 * g8['frac']:.1f}% of the "
               f"fp8 peak; with the SwiGLU epilogue {g8['swiglu_epilogue_ms']:.3f} ms; relative error against bf16 "
-              f"{g8['relative_error_vs_bf16']:.4f})", file=sys.stderr)
+              f"{g8['relative_error_vs_bf16']:.4f}), down {eg['down_fp8']['ms']:.3f} ms "
+              f"({eg['down_fp8']['TFLOP/s']:.0f} TFLOP/s)", file=sys.stderr)
         bw = eg["backward"]
         print(f"  expert GEMM backward: down dA fused with the combine backward {bw['down_input_grad_fused_combine_bwd_ms']:.3f}"
               f" ms (transpose {bw['weight_transpose_down_ms']:.3f}), gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, "
