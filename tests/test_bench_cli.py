@@ -1,0 +1,35 @@
+"""bench.py's command line on the CPU: it measures one GPU only, so any other
+GPU count (or a multi-rank launch) exits with status 2 and a message before
+touching a device, and the documented flags parse."""
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _run(args, env_extra=None):
+    env = dict(os.environ)
+    env.update(env_extra or {})
+    return subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], cwd=ROOT, env=env,
+                          capture_output=True, text=True, timeout=120)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = _run(["--gpus", "2", "--steps", "1", "--warmup", "0"])
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout == ""
+
+
+def test_multi_rank_launch_exits_with_a_message():
+    r = _run(["--steps", "1"], {"WORLD_SIZE": "2"})
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+
+
+def test_help_lists_the_driver_flags():
+    r = _run(["--help"])
+    assert r.returncode == 0
+    for flag in ("--gpus", "--steps", "--warmup", "--workload", "--cpu-tokens"):
+        assert flag in r.stdout
