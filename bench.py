@@ -394,37 +394,236 @@ def expert_gemm_leg(et, dev, stream, plan, X, reps: int = 3) -> dict:
                        "backward_frac": round(sw_bwd_gbs * 1e9 / HBM_PEAK, 4)}}
 
 
-def cpu_baseline(workload: str, seed: int, tokens: int) -> dict:
-    """The CPU restatement (oracle/, single thread) on the first `tokens`
-    tokens of the same workload, running the same five operations as one GPU
-    step.  Routing uses the workload's real logits.  The row operands are a block
-    of 1024 seeded random rows, tiled to the needed row counts; the row kernels
-    have no data-dependent control flow, so tiling changes no timing."""
+def load_shape(counts, token_offsets) -> dict:
+    """Per-token expert counts (k) and per-expert loads of a routing, from its
+    counts [E] and token_offsets [T+1] (host arrays)."""
+    import numpy as np
+    k = np.diff(np.asarray(token_offsets, np.int64))
+    c = np.sort(np.asarray(counts, np.int64))[::-1]
+    hist = np.bincount(k)
+    nz = c[c > 0]
+    return {"k_hist": {str(i): int(n) for i, n in enumerate(hist) if n},
+            "k_min": int(k.min()), "k_max": int(k.max()), "k_mean": round(float(k.mean()), 4),
+            "k_std": round(float(k.std()), 4),
+            "expert_load": {"max": int(c[0]), "median": int(np.median(c)), "min": int(c[-1]),
+                            "empty_experts": int((c == 0).sum()),
+                            "max_over_min_nonempty": round(float(nz[0] / nz[-1]), 2) if nz.size else None,
+                            "top8_share": round(float(c[:8].sum() / max(1, c.sum())), 4)}}
+
+
+def cpu_baseline(workload: str, step, reps: int = 3) -> dict:
+    """The CPU restatement (oracle/, C with OpenMP) timed on this host's cores
+    on the whole workload, on the very inputs of the GPU step (copied from the
+    device): route, dispatch, combine, combine backward with dlogits, dispatch
+    backward -- the five operations of one GPU step -- into preallocated
+    outputs.  One untimed warm-up pass (it also faults the output pages in),
+    then the median of `reps` timed passes.  Threads: OMP_NUM_THREADS if set
+    (the GPU box sets it to the CPU share of one GPU), else every core of this
+    process's affinity mask.  The CPU outputs are then compared with the GPU
+    step's: routing, Xp, Y, dYp, dX and dlogits bit for bit, dgate within one
+    binary32 ulp plus the binary64 summation floor."""
     import numpy as np
     import oracle
-    W = importlib.import_module("peer-review-agents_amd.workloads")
-    cfg = W.CONFIGS[workload]
-    lg, thr = W.router_inputs(workload, seed=seed)
-    lg = np.ascontiguousarray(lg[:tokens])
-    d, E = cfg["d"], cfg["E"]
-    r = oracle.route(lg, thr)
-    S = r.num_slots
-    conv = oracle.f32_to_bf16 if cfg["dtype"] == "bf16" else (lambda a: a)
-    blk = conv(W.randn_rows(1024, d, 1))
-    dyblk = conv(W.randn_rows(1024, d, 3, 0.02))
-    x, yp, dxp = np.resize(blk, (tokens, d)), np.resize(blk, (S, d)), np.resize(blk, (S, d))
-    dy = np.resize(dyblk, (tokens, d))
+    nproc = len(os.sched_getaffinity(0))
+    want = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
+    threads = oracle.set_threads(want)
+    T, d, E, S = step.T, step.d, step.E, step.S
+    u16 = lambda t: t.view(torch_mod().int16).cpu().numpy().view(np.uint16)  # noqa: E731
+    host = (lambda t: u16(t)) if step.act_bits == 16 else (lambda t: t.cpu().numpy())
+    lg, thr = step.logits.cpu().numpy(), step.thr.cpu().numpy()
+    x, yp, dy, dxp = host(step.X), host(step.YP), host(step.DY), host(step.DXP)
+    adt = x.dtype
+    xp, y, dyp = np.empty((S, d), adt), np.empty((T, d), adt), np.empty((S, d), adt)
+    dgate, dl, dx = np.empty(S, np.float32), np.empty((T, E), np.float32), np.empty((T, d), adt)
+
+    def one_pass():
+        r = oracle.route(lg, thr)
+        oracle.dispatch_fwd(x, r, out=xp)
+        oracle.combine_fwd(yp, r, T, out=y)
+        oracle.combine_bwd(dy, yp, r, E, want_dlogits=True, out=(dyp, dgate, dl))
+        oracle.dispatch_bwd(dxp, r, T, out=dx)
+        return r
+
     t0 = time.perf_counter()
-    r = oracle.route(lg, thr)
-    oracle.dispatch_fwd(x, r)
-    oracle.combine_fwd(yp, r, tokens)
-    oracle.combine_bwd(dy, yp, r, E, want_dlogits=True)
-    oracle.dispatch_bwd(dxp, r, tokens)
-    dt = time.perf_counter() - t0
-    return {"value": round(S / dt, 1), "unit": "slots/s", "cores": 1, "kind": "port",
-            "sample": f"first {tokens} of {cfg['T']} tokens of {workload} ({S} slots), one fwd+bwd pass "
-                      f"(route, dispatch, combine, combine backward with dlogits, dispatch backward) by "
-                      f"the C oracle on one host thread: {dt:.2f} s"}
+    r = one_pass()
+    warm = time.perf_counter() - t0
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        r = one_pass()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+
+    # full-size parity of the GPU step against these CPU outputs
+    step.sync_outputs()
+    bits_eq = lambda a, b: bool(np.array_equal(np.ascontiguousarray(a).view(np.uint8),  # noqa: E731
+                                               np.ascontiguousarray(b).view(np.uint8)))
+    gdg = step.DGATE.cpu().numpy().astype(np.float64)
+    dyf = dy.astype(np.float64) if adt == np.float32 else oracle.bf16_to_f32(dy).astype(np.float64)
+    ypf = yp.astype(np.float64) if adt == np.float32 else oracle.bf16_to_f32(yp).astype(np.float64)
+    mass = np.empty(S)
+    for a in range(0, S, 65536):              # sum_c |dY Yp| per slot, in blocks
+        b_ = min(S, a + 65536)
+        mass[a:b_] = np.abs(dyf[r.sorted_token[a:b_]] * ypf[a:b_]).sum(1)
+    del dyf, ypf
+    cdg = dgate.astype(np.float64)
+    err = np.abs(gdg - cdg)
+    parity = {
+        "routing_bit_exact": all(bits_eq(step.host_plan[f], getattr(r, f)) for f in
+                                 ("counts", "expert_offsets", "token_offsets", "sorted_token", "slot_gate",
+                                  "token_slot")),
+        "dispatch_bit_exact": bits_eq(host(step.XP), xp),
+        "combine_bit_exact": bits_eq(host(step.Y), y),
+        "combine_bwd_dyp_bit_exact": bits_eq(host(step.DYP), dyp),
+        "dlogits_bit_exact": bits_eq(step.DL.cpu().numpy(), dl),
+        "dispatch_bwd_bit_exact": bits_eq(host(step.DX), dx),
+        "dgate_within_bar": bool(np.all(err <= 2.0 ** -23 * np.abs(cdg) + 2 * d * 2.0 ** -53 * mass)),
+        "dgate_bit_equal_frac": round(float((gdg == cdg).mean()), 6),
+        "dgate_max_rel": float((err / np.maximum(np.abs(cdg), 1e-300)).max()),
+    }
+    return {"value": round(S / med, 1), "unit": "slots/s", "cores": threads, "nproc": nproc,
+            "kind": "port", "reps": reps, "rep_s": [round(t, 3) for t in times], "median_s": round(med, 4),
+            "warmup_s": round(warm, 3),
+            "sample": f"the whole {workload} step ({T} tokens, {S} slots, d={d}), on the GPU step's inputs: "
+                      f"route, dispatch, combine, combine backward with dlogits, dispatch backward by the C "
+                      f"oracle (OpenMP, {threads} threads of {nproc} in this process's CPU set), one warm-up "
+                      f"pass then the median of {reps}",
+            "full_size_parity_vs_gpu": parity}
+
+
+def torch_mod():
+    import torch
+    return torch
+
+
+class Step:
+    """One workload's resident buffers and its five stages, called through the
+    C ABI on one stream with the routed slot count as the slot capacity (so no
+    stage synchronises with the host)."""
+
+    def __init__(self, et, lib, dev, workload: str, seed: int):
+        import torch
+        W = importlib.import_module("peer-review-agents_amd.workloads")
+        self.lib, self.dev, self.workload = lib, dev, workload
+        cfg = W.CONFIGS[workload]
+        self.cfg = cfg
+        T, d, E = cfg["T"], cfg["d"], cfg["E"]
+        self.T, self.d, self.E = T, d, E
+        act = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+        self.act, self.b = act, (2 if act == torch.bfloat16 else 4)
+        self.act_bits = 16 if act == torch.bfloat16 else 32
+        self.dt_code = 1 if act == torch.bfloat16 else 0
+        lg_h, thr_h = W.router_inputs(workload, seed=seed)
+        self.logits = torch.from_numpy(lg_h).to(dev)
+        self.thr = torch.from_numpy(thr_h).to(dev)
+        plan = et.route(self.logits, self.thr)        # sizes the slot buffers (one sync, untimed)
+        S = self.S = plan.num_slots
+        self.shape = load_shape(plan.counts.cpu().numpy(), plan.token_offsets.cpu().numpy())
+        del plan
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.X = torch.randn(T, d, device=dev, generator=g).to(act)
+        self.YP = torch.randn(S, d, device=dev, generator=g).to(act)
+        self.DY = (torch.randn(T, d, device=dev, generator=g) * 0.02).to(act)
+        self.DXP = torch.randn(S, d, device=dev, generator=g).to(act)
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.counts, self.eoff, self.toff = torch.empty(E, **i32), torch.empty(E + 1, **i32), torch.empty(T + 1, **i32)
+        self.st, self.ts = torch.empty(S, **i32), torch.empty(S, **i32)
+        self.sg = torch.empty(S, dtype=torch.float32, device=dev)
+        self.wsb = et.route_workspace_bytes(T, E)
+        self.ws = torch.empty(self.wsb, dtype=torch.uint8, device=dev)
+        self.XP = torch.empty(S, d, dtype=act, device=dev)
+        self.Y = torch.empty(T, d, dtype=act, device=dev)
+        self.DYP = torch.empty(S, d, dtype=act, device=dev)
+        self.DGATE = torch.empty(S, dtype=torch.float32, device=dev)
+        self.DL = torch.empty(T, E, dtype=torch.float32, device=dev)
+        self.DX = torch.empty(T, d, dtype=act, device=dev)
+        self.bwsb = et.combine_backward_workspace_bytes(T, S, d, act)
+        self.BWS = torch.empty(max(self.bwsb, 8), dtype=torch.uint8, device=dev)
+        self.stream = torch.cuda.current_stream(dev)
+        self.host_plan = None
+
+    def stage(self, i, stream=None):
+        vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        sp = ctypes.c_void_p((stream or self.stream).cuda_stream)
+        L, T, E, d, S, dt = self.lib, self.T, self.E, self.d, self.S, self.dt_code
+        if i == 0:
+            rc = L.et_route(vp(self.logits), vp(self.thr), T, E, vp(self.counts), vp(self.eoff), vp(self.toff),
+                            vp(self.st), vp(self.sg), vp(self.ts), S, vp(self.ws), self.wsb, sp)
+        elif i == 1:
+            rc = L.et_dispatch_fwd(vp(self.X), T, d, dt, vp(self.toff), vp(self.ts), S, vp(self.XP), sp)
+        elif i == 2:
+            rc = L.et_combine_fwd(vp(self.YP), vp(self.sg), vp(self.toff), vp(self.ts), T, d, dt, S, vp(self.Y), sp)
+        elif i == 3:
+            rc = L.et_combine_bwd(vp(self.DY), vp(self.YP), vp(self.sg), vp(self.st), vp(self.toff), vp(self.ts),
+                                  vp(self.eoff), T, E, d, dt, S, vp(self.DYP), vp(self.DGATE), vp(self.DL),
+                                  vp(self.BWS), self.bwsb, sp)
+        else:
+            rc = L.et_dispatch_bwd(vp(self.DXP), vp(self.toff), vp(self.ts), T, d, dt, S, vp(self.DX), sp)
+        if rc != 0:
+            raise RuntimeError(f"{self.workload} stage {STAGES[i]} failed: {L.et_last_error().decode()}")
+
+    def timed(self, steps: int, warmup: int, stages) -> tuple:
+        """Per-stage HIP-event milliseconds (averaged over `steps`) and the
+        wall-clock milliseconds per step."""
+        import torch
+        if 0 not in stages:
+            self.stage(0)                             # the routing the other stages read
+        for _ in range(warmup):
+            for i in stages:
+                self.stage(i)
+        torch.cuda.synchronize()
+        if int(self.eoff[self.E]) != self.S:
+            raise RuntimeError("routing changed between runs")
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            ev[k][0].record(self.stream)
+            for j, i in enumerate(stages):
+                self.stage(i)
+                ev[k][j + 1].record(self.stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        stage_ms = {STAGES[i]: sum(ev[k][j].elapsed_time(ev[k][j + 1]) for k in range(steps)) / steps
+                    for j, i in enumerate(stages)}
+        return stage_ms, wall_ms
+
+    def sync_outputs(self):
+        """Host copies of the routing outputs of the last step."""
+        import torch
+        torch.cuda.synchronize()
+        self.host_plan = {"counts": self.counts.cpu().numpy(), "expert_offsets": self.eoff.cpu().numpy(),
+                          "token_offsets": self.toff.cpu().numpy(), "sorted_token": self.st.cpu().numpy(),
+                          "slot_gate": self.sg.cpu().numpy(), "token_slot": self.ts.cpu().numpy()}
+
+    def summary(self, stages, stage_ms, wall_ms) -> dict:
+        ab = algorithmic_bytes(self.T, self.E, self.S, self.d, self.b)
+        nbytes = sum(ab[STAGES[i]] for i in stages)
+        return {"workload": f"{self.workload}: T={self.T} d={self.d} E={self.E} {self.cfg['dtype']}, "
+                            f"thresholds {self.cfg['thr']}",
+                "stages": [STAGES[i] for i in stages], "slots": self.S, "mean_k": round(self.S / self.T, 4),
+                "ms_per_step": round(wall_ms, 4), "slots_per_s": round(self.S / (wall_ms * 1e-3), 1),
+                "algorithmic_bytes": nbytes, "hbm_frac": round(nbytes / (wall_ms * 1e-3) / HBM_PEAK, 4),
+                "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()}, "load_shape": self.shape}
+
+    def release(self):
+        for name in ("X", "YP", "DY", "DXP", "XP", "Y", "DYP", "DGATE", "DL", "DX", "BWS", "ws", "logits"):
+            setattr(self, name, None)
+
+
+def extra_workload(et, lib, dev, workload: str, seed: int, stages, steps: int = 10, warmup: int = 3) -> dict:
+    """A full-size step of another configuration, timed like the headline
+    step (HIP events per stage, wall clock per step), its buffers freed after."""
+    import torch
+    st = Step(et, lib, dev, workload, seed)
+    stage_ms, wall_ms = st.timed(steps, warmup, stages)
+    out = st.summary(stages, stage_ms, wall_ms)
+    out["steps"] = steps
+    st.release()
+    del st
+    torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -434,8 +633,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-tokens", type=int, default=32768,
-                    help="tokens in the CPU baseline's sample (0 skips it)")
+    ap.add_argument("--cpu-reps", type=int, default=3,
+                    help="timed passes of the CPU baseline after its warm-up (0 skips it)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the side measurements (other configs, router, expert GEMM)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -444,7 +645,6 @@ def main() -> int:
               "run with --gpus 1.", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     et = importlib.import_module("peer-review-agents_amd")
@@ -452,86 +652,19 @@ def main() -> int:
     lib = et.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    cfg = W.CONFIGS[args.workload]
-    T, d, E = cfg["T"], cfg["d"], cfg["E"]
-    act = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
-    b = 2 if act == torch.bfloat16 else 4
-    dt_code = 1 if act == torch.bfloat16 else 0
-
-    # ---- resident inputs ------------------------------------------------------
-    lg_h, thr_h = W.router_inputs(args.workload, seed=args.seed)
-    logits = torch.from_numpy(lg_h).to(dev)
-    thr = torch.from_numpy(thr_h).to(dev)
-    plan = et.route(logits, thr)                 # sizes the slot buffers (one sync, untimed)
-    S = plan.num_slots
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed)
-    X = torch.randn(T, d, device=dev, generator=g).to(act)
-    YP = torch.randn(S, d, device=dev, generator=g).to(act)
-    DY = (torch.randn(T, d, device=dev, generator=g) * 0.02).to(act)
-    DXP = torch.randn(S, d, device=dev, generator=g).to(act)
-    i32 = dict(dtype=torch.int32, device=dev)
-    counts, eoff, toff = torch.empty(E, **i32), torch.empty(E + 1, **i32), torch.empty(T + 1, **i32)
-    st, ts = torch.empty(S, **i32), torch.empty(S, **i32)
-    sg = torch.empty(S, dtype=torch.float32, device=dev)
-    wsb = et.route_workspace_bytes(T, E)
-    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-    XP = torch.empty(S, d, dtype=act, device=dev)
-    Y = torch.empty(T, d, dtype=act, device=dev)
-    DYP = torch.empty(S, d, dtype=act, device=dev)
-    DGATE = torch.empty(S, dtype=torch.float32, device=dev)
-    DL = torch.empty(T, E, dtype=torch.float32, device=dev)
-    DX = torch.empty(T, d, dtype=act, device=dev)
-    bwsb = et.combine_backward_workspace_bytes(T, S, d, act)
-    BWS = torch.empty(max(bwsb, 1), dtype=torch.uint8, device=dev)
-    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    P = [vp(t) for t in (logits, thr, counts, eoff, toff, st, sg, ts, ws, X, XP, YP, Y, DY, DYP, DGATE, DL,
-                         DXP, DX, BWS)]
-    (p_lg, p_thr, p_cnt, p_eo, p_to, p_st, p_sg, p_ts, p_ws, p_x, p_xp, p_yp, p_y, p_dy, p_dyp, p_dg, p_dl,
-     p_dxp, p_dx, p_bws) = P
-
-    def stage(i, sp=sp):
-        if i == 0:
-            rc = lib.et_route(p_lg, p_thr, T, E, p_cnt, p_eo, p_to, p_st, p_sg, p_ts, S, p_ws, wsb, sp)
-        elif i == 1:
-            rc = lib.et_dispatch_fwd(p_x, T, d, dt_code, p_to, p_ts, S, p_xp, sp)
-        elif i == 2:
-            rc = lib.et_combine_fwd(p_yp, p_sg, p_to, p_ts, T, d, dt_code, S, p_y, sp)
-        elif i == 3:
-            rc = lib.et_combine_bwd(p_dy, p_yp, p_sg, p_st, p_to, p_ts, p_eo, T, E, d, dt_code, S, p_dyp, p_dg,
-                                    p_dl, p_bws, bwsb, sp)
-        else:
-            rc = lib.et_dispatch_bwd(p_dxp, p_to, p_ts, T, d, dt_code, S, p_dx, sp)
-        if rc != 0:
-            raise RuntimeError(f"stage {STAGES[i]} failed: {lib.et_last_error().decode()}")
+    print(f"bench: workload {args.workload}, {args.steps} steps after {args.warmup} warm-up", file=sys.stderr,
+          flush=True)
+    step = Step(et, lib, dev, args.workload, args.seed)
+    T, d, E, S, cfg = step.T, step.d, step.E, step.S, step.cfg
+    stream = step.stream
+    all_stages = list(range(len(STAGES)))
 
     copy_ref = copy_ceiling(dev, stream)
-    for _ in range(args.warmup):
-        for i in range(len(STAGES)):
-            stage(i)
-    torch.cuda.synchronize()
-    assert int(eoff[E]) == S, "routing changed between runs"
 
     # ---- timed region -----------------------------------------------------------
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        ev[k][0].record(stream)
-        for i in range(len(STAGES)):
-            stage(i)
-            ev[k][i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    stage_ms, ms_per_step = step.timed(args.steps, args.warmup, all_stages)
 
-    stage_ms = {name: 0.0 for name in STAGES}
-    for k in range(args.steps):
-        for i, name in enumerate(STAGES):
-            stage_ms[name] += ev[k][i].elapsed_time(ev[k][i + 1]) / args.steps
-    ms_per_step = wall * 1e3 / args.steps
-    abytes = algorithmic_bytes(T, E, S, d, b)
+    abytes = algorithmic_bytes(T, E, S, d, step.b)
     step_bytes = sum(abytes.values())
     kernels = {}
     for name in STAGES:
@@ -553,9 +686,9 @@ def main() -> int:
     # capture holds no host synchronisation.
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        cs = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        for i in range(len(STAGES)):
-            stage(i, cs)
+        cs = torch.cuda.current_stream(dev)
+        for i in all_stages:
+            step.stage(i, cs)
     graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -563,60 +696,83 @@ def main() -> int:
         graph.replay()
     torch.cuda.synchronize()
     graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    assert int(eoff[E]) == S, "routing changed under graph replay"
+    assert int(step.eoff[E]) == S, "routing changed under graph replay"
     del graph
     graph_replay = {"ms_per_step": round(graph_ms, 4), "slots_per_s": round(S / (graph_ms * 1e-3), 1),
                     "hbm_frac": round(step_bytes / (graph_ms * 1e-3) / HBM_PEAK, 4)}
+    slots_per_s = S / (ms_per_step * 1e-3)
+    for name in STAGES:
+        k = kernels[name]
+        print(f"  {name:13s} {k['ms']:8.4f} ms  {k['GB/s']:8.1f} GB/s  {100 * k['frac']:5.1f}% of peak",
+              file=sys.stderr)
+    print(f"  copy ref      {copy_ref['ms']:8.4f} ms  {copy_ref['GB/s']:8.1f} GB/s  "
+          f"{100 * copy_ref['frac']:5.1f}% of peak ({copy_ref['kernel']}, {copy_ref['bytes']} B)",
+          file=sys.stderr)
+    print(f"  step {ms_per_step:.4f} ms, {slots_per_s / 1e6:.2f} M slots/s, "
+          f"{100 * step_bytes / (ms_per_step * 1e-3) / HBM_PEAK:.1f}% of HBM peak; replayed as a HIP graph "
+          f"{graph_ms:.4f} ms ({100 * graph_replay['hbm_frac']:.1f}%)", file=sys.stderr, flush=True)
 
-    dyn = None
-    if cfg["thr"] == "ema":
-        dyn = threshold_dynamics(et, W, dev, stream, args.workload, args.seed)
-        print(f"  threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
+    # ---- side measurements (after the timed region) -------------------------------
+    dyn = rp = rb = eg = None
+    extras = {}
+    if not args.no_extras:
+        dyn = threshold_dynamics(et, W, dev, stream, "C5", args.seed)
+        print(f"  C5 threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
               f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
               f"{dyn['mean_k_last_step']}; all steps replayed as one HIP graph "
-              f"{dyn['graph_replay_ms_per_step']:.4f} ms per step", file=sys.stderr)
-
-    rp = None
-    if act == torch.bfloat16 and E <= 256:
-        rp = router_producer(et, dev, stream, X, E)
-        print(f"  router producer: logits {rp['us']:.1f} us ({rp['GB/s']:.0f} GB/s, {100 * rp['frac']:.1f}% of "
-              f"peak; torch bf16 linear {rp['torch_linear_bf16_us']:.1f} us), fused route {rp['fused_route_us']:.1f}"
-              f" us vs logits + route {rp['logits_then_route_us']:.1f} us", file=sys.stderr)
-
-    plan_obj = et.RoutingPlan(counts, eoff, toff, st, sg, ts, T, E, S, S)
-    rb = router_backward(et, dev, stream, plan_obj, X, DXP, DGATE, DL)
-    print(f"  router backward: dispatch_bwd {rb['dispatch_bwd_us']:.1f} us -> with the router input gradient "
-          f"{rb['dispatch_bwd_router_us']:.1f} us" + (f"; dW {rb['router_wgrad_us']:.1f} us "
-          f"({100 * rb['router_wgrad_frac']:.1f}% of peak; torch f32 mm {rb['torch_mm_f32_wgrad_us']:.1f} us)"
-          if "router_wgrad_us" in rb else ""), file=sys.stderr)
-
-    eg = None
-    if act == torch.bfloat16 and d % 8 == 0 and S > 0:
-        eg = expert_gemm_leg(et, dev, stream, plan_obj, X)
-        gu, dn = eg["gate_up"], eg["down"]
-        print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; with the SwiGLU "
-              f"epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} ms + dispatch "
-              f"{gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; torch grouped "
-              f"{dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
-        g8 = eg["gate_up_fp8"]
-        print(f"  expert GEMM fp8: gate/up {g8['ms']:.3f} ms ({g8['TFLOP/s']:.0f} TFLOP/s, {100 * g8['frac']:.1f}% of the "
-              f"fp8 peak; with the SwiGLU epilogue {g8['swiglu_epilogue_ms']:.3f} ms; relative error against bf16 "
-              f"{g8['relative_error_vs_bf16']:.4f}), down {eg['down_fp8']['ms']:.3f} ms "
-              f"({eg['down_fp8']['TFLOP/s']:.0f} TFLOP/s)", file=sys.stderr)
-        bw = eg["backward"]
-        print(f"  expert GEMM backward: down dA fused with the combine backward {bw['down_input_grad_fused_combine_bwd_ms']:.3f}"
-              f" ms (transpose {bw['weight_transpose_down_ms']:.3f}), gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, "
-              f"dW gate/up {bw['gate_up_weight_grad_ms']:.3f} ms (torch grouped {bw['torch_grouped_mm_gate_up_weight_grad_ms']}"
-              f"), dW down {bw['down_weight_grad_ms']:.3f} ms", file=sys.stderr)
-        sw = eg["swiglu"]
-        print(f"  SwiGLU for training: forward {sw['forward_ms']:.3f} ms ({100 * sw['forward_frac']:.1f}% of peak), "
-              f"backward {sw['backward_ms']:.3f} ms ({100 * sw['backward_frac']:.1f}% of peak)", file=sys.stderr)
+              f"{dyn['graph_replay_ms_per_step']:.4f} ms per step", file=sys.stderr, flush=True)
+        if step.act == torch.bfloat16 and E <= 256:
+            rp = router_producer(et, dev, stream, step.X, E)
+            print(f"  router producer: logits {rp['us']:.1f} us ({rp['GB/s']:.0f} GB/s, {100 * rp['frac']:.1f}% of "
+                  f"peak; torch bf16 linear {rp['torch_linear_bf16_us']:.1f} us), fused route "
+                  f"{rp['fused_route_us']:.1f} us vs logits + route {rp['logits_then_route_us']:.1f} us",
+                  file=sys.stderr, flush=True)
+        plan_obj = et.RoutingPlan(step.counts, step.eoff, step.toff, step.st, step.sg, step.ts, T, E, S, S)
+        rb = router_backward(et, dev, stream, plan_obj, step.X, step.DXP, step.DGATE, step.DL)
+        print(f"  router backward: dispatch_bwd {rb['dispatch_bwd_us']:.1f} us -> with the router input gradient "
+              f"{rb['dispatch_bwd_router_us']:.1f} us" + (f"; dW {rb['router_wgrad_us']:.1f} us "
+              f"({100 * rb['router_wgrad_frac']:.1f}% of peak; torch f32 mm {rb['torch_mm_f32_wgrad_us']:.1f} us)"
+              if "router_wgrad_us" in rb else ""), file=sys.stderr, flush=True)
+        if step.act == torch.bfloat16 and d % 8 == 0 and S > 0:
+            eg = expert_gemm_leg(et, dev, stream, plan_obj, step.X)
+            gu, dn = eg["gate_up"], eg["down"]
+            print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; with the "
+                  f"SwiGLU epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} "
+                  f"ms + dispatch {gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; "
+                  f"torch grouped {dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
+            g8 = eg["gate_up_fp8"]
+            print(f"  expert GEMM fp8: gate/up {g8['ms']:.3f} ms ({g8['TFLOP/s']:.0f} TFLOP/s, {100 * g8['frac']:.1f}% "
+                  f"of the fp8 peak; with the SwiGLU epilogue {g8['swiglu_epilogue_ms']:.3f} ms; relative error "
+                  f"against bf16 {g8['relative_error_vs_bf16']:.4f}), down {eg['down_fp8']['ms']:.3f} ms "
+                  f"({eg['down_fp8']['TFLOP/s']:.0f} TFLOP/s)", file=sys.stderr)
+            bw = eg["backward"]
+            print(f"  expert GEMM backward: down dA fused with the combine backward "
+                  f"{bw['down_input_grad_fused_combine_bwd_ms']:.3f} ms (transpose {bw['weight_transpose_down_ms']:.3f}),"
+                  f" gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, dW gate/up {bw['gate_up_weight_grad_ms']:.3f} ms "
+                  f"(torch grouped {bw['torch_grouped_mm_gate_up_weight_grad_ms']}), dW down "
+                  f"{bw['down_weight_grad_ms']:.3f} ms", file=sys.stderr)
+            sw = eg["swiglu"]
+            print(f"  SwiGLU for training: forward {sw['forward_ms']:.3f} ms ({100 * sw['forward_frac']:.1f}% of peak), "
+                  f"backward {sw['backward_ms']:.3f} ms ({100 * sw['backward_frac']:.1f}% of peak)", file=sys.stderr,
+                  flush=True)
+        # the other row configurations at full size: C2 (variable k, all five
+        # stages) and C4 (one GPU's EP=8 expert share, backward only)
+        for name, stages in (("C2", all_stages), ("C4", [3, 4])):
+            if name == args.workload:
+                continue
+            extras[name] = extra_workload(et, lib, dev, name, args.seed, stages)
+            x = extras[name]
+            print(f"  {name} full size ({'+'.join(x['stages'])}): {x['ms_per_step']:.4f} ms per step, "
+                  f"{x['slots_per_s'] / 1e6:.2f} M slots/s, {100 * x['hbm_frac']:.1f}% of HBM peak, mean k "
+                  f"{x['mean_k']}", file=sys.stderr, flush=True)
 
     cpu = None
-    if args.cpu_tokens > 0:
-        cpu = cpu_baseline(args.workload, args.seed, min(args.cpu_tokens, T))
+    if args.cpu_reps > 0:
+        cpu = cpu_baseline(args.workload, step, reps=args.cpu_reps)
+        print(f"  CPU baseline: {cpu['value'] / 1e6:.3f} M slots/s ({cpu['median_s']:.3f} s per pass, "
+              f"{cpu['cores']} threads of {cpu['nproc']}); full-size parity vs GPU: "
+              f"{cpu['full_size_parity_vs_gpu']}", file=sys.stderr, flush=True)
 
-    slots_per_s = S / (ms_per_step * 1e-3)
     out = {
         "metric": METRIC,
         "value": round(slots_per_s, 1),
@@ -636,25 +792,17 @@ def main() -> int:
         "hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / HBM_PEAK, 4),
         "step_bytes": step_bytes,
         "roofline": roofline,
+        "load_shape": step.shape,
         "graph_replay": graph_replay,
         "cpu_baseline": cpu,
         "copy_ceiling": copy_ref,
+        "other_configs": extras or None,
         "threshold_dynamics": dyn,
         "router_producer": rp,
         "router_backward": rb,
         "expert_gemm": eg,
         "kernels": kernels,
     }
-    for name in STAGES:
-        k = kernels[name]
-        print(f"  {name:13s} {k['ms']:8.4f} ms  {k['GB/s']:8.1f} GB/s  {100 * k['frac']:5.1f}% of peak",
-              file=sys.stderr)
-    print(f"  copy ref      {copy_ref['ms']:8.4f} ms  {copy_ref['GB/s']:8.1f} GB/s  "
-          f"{100 * copy_ref['frac']:5.1f}% of peak ({copy_ref['kernel']}, {copy_ref['bytes']} B)",
-          file=sys.stderr)
-    print(f"  step {ms_per_step:.4f} ms, {slots_per_s / 1e6:.2f} M slots/s, "
-          f"{100 * out['hbm_frac']:.1f}% of HBM peak; replayed as a HIP graph {graph_ms:.4f} ms "
-          f"({100 * graph_replay['hbm_frac']:.1f}%)", file=sys.stderr)
     print(json.dumps(out), flush=True)
     return 0
 

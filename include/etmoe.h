@@ -121,14 +121,17 @@ int et_combine_fwd(const void* yp, const float* slot_gate, const int32_t* token_
                    int64_t slot_capacity, void* y, void* stream);
 
 /* Bytes of device workspace et_combine_bwd needs: slot_capacity * ceil(d * elem / 1024)
- * floats when a row is a whole number of 16-byte chunks, else 0. */
+ * doubles when a row is a whole number of 16-byte chunks, else 0.  The
+ * workspace must be 8-byte aligned. */
 size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype);
 
 /*
  * Combine backward (fused): for every slot s of token t = token(s), expert e:
  *   dYp[s, c]     = cast(slot_gate[s] * dY[t, c])
- *   dgate[s]      = sum_c dY[t, c] * Yp[s, c]            (binary32 accumulate)
- *   dlogits[t, e] = dgate[s] * g * (1 - g), g = slot_gate[s]; 0 elsewhere
+ *   dgate[s]      = sum_c dY[t, c] * Yp[s, c], accumulated in binary64 (every
+ *                   product is exact there) and rounded once to binary32
+ *   dlogits[t, e] = dgate[s] * (g * (1 - g)) in binary32, g = slot_gate[s];
+ *                   0 elsewhere
  * dlogits (f32 [T, E]) may be NULL.
  * workspace holds the per-piece partial dot products (et_combine_bwd_workspace_bytes);
  * it may be NULL when that size is 0.

@@ -85,10 +85,18 @@ def lib() -> ctypes.CDLL:
         L.oracle_combine_bwd.restype = None
         L.oracle_combine_bwd.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64,
                                          ctypes.c_int, _p, _p, _p]
+        L.oracle_set_threads.restype = ctypes.c_int
+        L.oracle_set_threads.argtypes = [ctypes.c_int]
         L.oracle_threshold_update.restype = _i64
         L.oracle_threshold_update.argtypes = [_p, _p, _i64, _i64, _i64, ctypes.c_float, _p]
         _lib = L
     return _lib
+
+
+def set_threads(n: int) -> int:
+    """Threads of the oracle's parallel loops (OpenMP); returns the count in
+    use.  Results are the same bits for any count."""
+    return int(lib().oracle_set_threads(int(n)))
 
 
 def _ptr(a: np.ndarray | None):
@@ -245,30 +253,39 @@ def route(logits: np.ndarray, thr: np.ndarray) -> Routing:
 # dispatch / combine
 # --------------------------------------------------------------------------- #
 
-def dispatch_fwd(x: np.ndarray, r: Routing) -> np.ndarray:
+def _out(out, shape, dtype):
+    """A caller-supplied output array (checked), or a new zeroed one."""
+    if out is None:
+        return np.zeros(shape, dtype)
+    if out.shape != tuple(shape) or out.dtype != dtype or not out.flags.c_contiguous:
+        raise ValueError(f"out must be a contiguous {dtype} array of shape {tuple(shape)}")
+    return out
+
+
+def dispatch_fwd(x: np.ndarray, r: Routing, out: np.ndarray | None = None) -> np.ndarray:
     dt = _act_dt(x)
     x = np.ascontiguousarray(x)
     T, d = x.shape
-    xp = np.zeros((r.num_slots, d), x.dtype)
+    xp = _out(out, (r.num_slots, d), x.dtype)
     lib().oracle_dispatch_fwd(_ptr(x), T, d, dt, _ptr(r.token_offsets), _ptr(r.token_slot), _ptr(xp))
     return xp
 
 
-def combine_fwd(yp: np.ndarray, r: Routing, T: int) -> np.ndarray:
+def combine_fwd(yp: np.ndarray, r: Routing, T: int, out: np.ndarray | None = None) -> np.ndarray:
     dt = _act_dt(yp)
     yp = np.ascontiguousarray(yp)
     d = yp.shape[1]
-    y = np.zeros((T, d), yp.dtype)
+    y = _out(out, (T, d), yp.dtype)
     lib().oracle_combine_fwd(_ptr(yp), _ptr(r.slot_gate), _ptr(r.token_offsets),
                              _ptr(r.token_slot), T, d, dt, _ptr(y))
     return y
 
 
-def dispatch_bwd(dxp: np.ndarray, r: Routing, T: int) -> np.ndarray:
+def dispatch_bwd(dxp: np.ndarray, r: Routing, T: int, out: np.ndarray | None = None) -> np.ndarray:
     dt = _act_dt(dxp)
     dxp = np.ascontiguousarray(dxp)
     d = dxp.shape[1]
-    dx = np.zeros((T, d), dxp.dtype)
+    dx = _out(out, (T, d), dxp.dtype)
     lib().oracle_dispatch_bwd(_ptr(dxp), _ptr(r.token_offsets), _ptr(r.token_slot), T, d, dt, _ptr(dx))
     return dx
 
@@ -290,15 +307,18 @@ def dispatch_bwd_router(dxp: np.ndarray, r: Routing, T: int, dgate: np.ndarray, 
     return dx
 
 
-def combine_bwd(dy: np.ndarray, yp: np.ndarray, r: Routing, E: int, want_dlogits: bool = False):
+def combine_bwd(dy: np.ndarray, yp: np.ndarray, r: Routing, E: int, want_dlogits: bool = False,
+                out: tuple | None = None):
+    """(dYp, dgate, dlogits or None); `out` optionally supplies the arrays."""
     dt = _act_dt(dy)
     assert _act_dt(yp) == dt
     dy = np.ascontiguousarray(dy)
     yp = np.ascontiguousarray(yp)
     T, d = dy.shape
-    dyp = np.zeros((r.num_slots, d), dy.dtype)
-    dgate = np.zeros(r.num_slots, np.float32)
-    dlogits = np.zeros((T, E), np.float32) if want_dlogits else None
+    o = out if out is not None else (None, None, None)
+    dyp = _out(o[0], (r.num_slots, d), dy.dtype)
+    dgate = _out(o[1], (r.num_slots,), np.float32)
+    dlogits = _out(o[2], (T, E), np.float32) if want_dlogits else None
     lib().oracle_combine_bwd(_ptr(dy), _ptr(yp), _ptr(r.slot_gate), _ptr(r.sorted_token),
                              _ptr(r.expert_offsets), T, E, d, dt, _ptr(dyp), _ptr(dgate),
                              _ptr(dlogits))

@@ -25,11 +25,33 @@
  * Floating point: build with -ffp-contract=off.  fmaf() is used exactly where
  * the specification says "fused multiply-add"; every other + - * / is a single
  * IEEE binary32 operation with round-to-nearest-even.
+ *
+ * Threads: built with OpenMP, the row, routing and threshold functions split
+ * their independent outputs (tokens, slots, experts) over threads.  Every
+ * output element is still computed by one thread, in the order its comment
+ * states, so the results are the same bits for any thread count
+ * (oracle_set_threads; OMP_NUM_THREADS otherwise).
  */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Threads for the parallel loops (n < 1 leaves the setting unchanged);
+ * returns the number now in use (1 without OpenMP). */
+int oracle_set_threads(int n)
+{
+#ifdef _OPENMP
+    if (n >= 1) omp_set_num_threads(n);
+    return omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}
 
 #define OR_DT_F32 0
 #define OR_DT_BF16 1
@@ -220,6 +242,7 @@ int64_t oracle_select(const float* logits, const float* thr, int64_t T, int64_t 
                       uint8_t* sel, float* score)
 {
     int64_t S = 0;
+#pragma omp parallel for schedule(static) reduction(+ : S)
     for (int64_t t = 0; t < T; ++t) {
         int64_t k = 0;
         for (int64_t e = 0; e < E; ++e) {
@@ -269,17 +292,22 @@ int64_t oracle_route(const float* logits, const float* thr, int64_t T, int64_t E
 
     int64_t S = oracle_select(logits, thr, T, E, sel, score);
 
-    /* histogram */
-    for (int64_t e = 0; e < E; ++e) counts[e] = 0;
-    for (int64_t t = 0; t < T; ++t)
-        for (int64_t e = 0; e < E; ++e) counts[e] += sel[t * E + e];
+    /* histogram (one expert column per iteration) */
+#pragma omp parallel for schedule(static)
+    for (int64_t e = 0; e < E; ++e) {
+        int32_t c = 0;
+        for (int64_t t = 0; t < T; ++t) c += sel[t * E + e];
+        counts[e] = c;
+    }
     /* exclusive scan */
     expert_offsets[0] = 0;
     for (int64_t e = 0; e < E; ++e) expert_offsets[e + 1] = expert_offsets[e] + counts[e];
 
-    /* slots in (expert, token) lexicographic order */
-    int64_t s = 0;
-    for (int64_t e = 0; e < E; ++e)
+    /* slots in (expert, token) lexicographic order: expert e's slots start at
+     * expert_offsets[e] and follow its tokens in ascending order */
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t e = 0; e < E; ++e) {
+        int64_t s = expert_offsets[e];
         for (int64_t t = 0; t < T; ++t) {
             if (!sel[t * E + e]) continue;
             slot_of[t * E + e] = (int32_t)s;
@@ -289,18 +317,27 @@ int64_t oracle_route(const float* logits, const float* thr, int64_t T, int64_t E
             }
             ++s;
         }
+    }
 
-    /* token-major CSR */
-    int64_t pos = 0;
+    /* token-major CSR: token_offsets is the exclusive scan of the per-token
+     * counts; token t's entries list its slots in ascending expert order */
+#pragma omp parallel for schedule(static)
     for (int64_t t = 0; t < T; ++t) {
-        token_offsets[t] = (int32_t)pos;
+        int32_t k = 0;
+        for (int64_t e = 0; e < E; ++e) k += sel[t * E + e];
+        token_offsets[t + 1] = k;
+    }
+    token_offsets[0] = 0;
+    for (int64_t t = 0; t < T; ++t) token_offsets[t + 1] += token_offsets[t];
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+        int64_t pos = token_offsets[t];
         for (int64_t e = 0; e < E; ++e) {
             if (!sel[t * E + e]) continue;
             if (pos < slot_capacity) token_slot[pos] = slot_of[t * E + e];
             ++pos;
         }
     }
-    token_offsets[T] = (int32_t)pos;
 
     free(sel); free(score); free(slot_of);
     return S;
@@ -315,6 +352,7 @@ void oracle_dispatch_fwd(const void* x, int64_t T, int64_t d, int dt,
                          const int32_t* token_offsets, const int32_t* token_slot, void* xp)
 {
     size_t row = (size_t)d * (dt == OR_DT_BF16 ? 2 : 4);
+#pragma omp parallel for schedule(static)
     for (int64_t t = 0; t < T; ++t)
         for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j)
             memcpy((char*)xp + (size_t)token_slot[j] * row, (const char*)x + (size_t)t * row, row);
@@ -327,17 +365,21 @@ void oracle_dispatch_fwd(const void* x, int64_t T, int64_t d, int dt,
 void oracle_combine_fwd(const void* yp, const float* gate, const int32_t* token_offsets,
                         const int32_t* token_slot, int64_t T, int64_t d, int dt, void* y)
 {
-    float* acc = (float*)malloc((size_t)(d ? d : 1) * sizeof(float));
-    for (int64_t t = 0; t < T; ++t) {
-        for (int64_t c = 0; c < d; ++c) acc[c] = 0.0f;
-        for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j) {
-            int64_t s = token_slot[j];
-            float g = gate ? gate[s] : 1.0f;
-            for (int64_t c = 0; c < d; ++c) acc[c] = fmaf(g, load_elem(yp, s * d + c, dt), acc[c]);
+#pragma omp parallel
+    {
+        float* acc = (float*)malloc((size_t)(d ? d : 1) * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < T; ++t) {
+            for (int64_t c = 0; c < d; ++c) acc[c] = 0.0f;
+            for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j) {
+                int64_t s = token_slot[j];
+                float g = gate ? gate[s] : 1.0f;
+                for (int64_t c = 0; c < d; ++c) acc[c] = fmaf(g, load_elem(yp, s * d + c, dt), acc[c]);
+            }
+            for (int64_t c = 0; c < d; ++c) store_elem(y, t * d + c, acc[c], dt);
         }
-        for (int64_t c = 0; c < d; ++c) store_elem(y, t * d + c, acc[c], dt);
+        free(acc);
     }
-    free(acc);
 }
 
 void oracle_dispatch_bwd(const void* dxp, const int32_t* token_offsets, const int32_t* token_slot,
@@ -357,30 +399,37 @@ void oracle_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, c
                                 const int32_t* expert_offsets, int64_t E, const float* gate,
                                 const float* dgate, const void* w, int64_t T, int64_t d, int dt, void* dx)
 {
-    float* acc = (float*)malloc((size_t)(d ? d : 1) * sizeof(float));
-    for (int64_t t = 0; t < T; ++t) {
-        for (int64_t c = 0; c < d; ++c) acc[c] = 0.0f;
-        for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j) {
-            int64_t s = token_slot[j];
-            int64_t e = 0;
-            while (e + 1 < E && expert_offsets[e + 1] <= s) ++e;
-            float g = gate[s];
-            float dl = dgate[s] * (g * (1.0f - g));
-            for (int64_t c = 0; c < d; ++c) {
-                acc[c] = acc[c] + load_elem(dxp, s * d + c, dt);
-                acc[c] = fmaf(dl, load_elem(w, e * d + c, dt), acc[c]);
+#pragma omp parallel
+    {
+        float* acc = (float*)malloc((size_t)(d ? d : 1) * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < T; ++t) {
+            for (int64_t c = 0; c < d; ++c) acc[c] = 0.0f;
+            for (int32_t j = token_offsets[t]; j < token_offsets[t + 1]; ++j) {
+                int64_t s = token_slot[j];
+                int64_t e = 0;
+                while (e + 1 < E && expert_offsets[e + 1] <= s) ++e;
+                float g = gate[s];
+                float dl = dgate[s] * (g * (1.0f - g));
+                for (int64_t c = 0; c < d; ++c) {
+                    acc[c] = acc[c] + load_elem(dxp, s * d + c, dt);
+                    acc[c] = fmaf(dl, load_elem(w, e * d + c, dt), acc[c]);
+                }
             }
+            for (int64_t c = 0; c < d; ++c) store_elem(dx, t * d + c, acc[c], dt);
         }
-        for (int64_t c = 0; c < d; ++c) store_elem(dx, t * d + c, acc[c], dt);
+        free(acc);
     }
-    free(acc);
 }
 
 /* Backward of combine for slot s (token t = sorted_token[s], expert e):
  *   dYp[s,c]   = cast(gate[s] * dY[t,c])       one binary32 multiply, then cast
- *   dgate[s]   = sum_c dY[t,c] * Yp[s,c]        (accumulated here in double; the
- *                                               product path may use any order)
- *   dlogits[t,e] = dgate[s] * g * (1 - g), g = gate[s]   (selected pairs)
+ *   dgate[s]   = sum_c dY[t,c] * Yp[s,c]        accumulated in double in
+ *                                               ascending c (every product of
+ *                                               two binary32 values is exact in
+ *                                               double), rounded once to float
+ *   dlogits[t,e] = dgate[s] * (g * (1 - g))     binary32, from the rounded
+ *                                               dgate, g = gate[s] (selected pairs)
  *   dlogits[t,e] = 0                                      (all other pairs)
  * dlogits may be NULL. */
 void oracle_combine_bwd(const void* dy, const void* yp, const float* gate,
@@ -388,22 +437,32 @@ void oracle_combine_bwd(const void* dy, const void* yp, const float* gate,
                         int64_t T, int64_t E, int64_t d, int dt,
                         void* dyp, float* dgate, float* dlogits)
 {
-    if (dlogits) for (int64_t i = 0; i < T * E; ++i) dlogits[i] = 0.0f;
-    for (int64_t e = 0; e < E; ++e)
-        for (int64_t s = expert_offsets[e]; s < expert_offsets[e + 1]; ++s) {
-            int64_t t = sorted_token[s];
-            double dot = 0.0;
-            for (int64_t c = 0; c < d; ++c) {
-                float g_dy = load_elem(dy, t * d + c, dt);
-                dot += (double)g_dy * (double)load_elem(yp, s * d + c, dt);
-                store_elem(dyp, s * d + c, gate[s] * g_dy, dt);
-            }
-            dgate[s] = (float)dot;
-            if (dlogits) {
-                double g = gate[s];
-                dlogits[t * E + e] = (float)(dot * (g * (1.0 - g)));
-            }
+    if (dlogits) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < T * E; ++i) dlogits[i] = 0.0f;
+    }
+    const int64_t S = expert_offsets[E];
+#pragma omp parallel for schedule(static)
+    for (int64_t s = 0; s < S; ++s) {
+        int64_t lo = 0, hi = E;             /* expert e: expert_offsets[e] <= s < expert_offsets[e + 1] */
+        while (hi - lo > 1) {
+            int64_t mid = (lo + hi) / 2;
+            if (expert_offsets[mid] <= s) lo = mid; else hi = mid;
         }
+        const int64_t e = lo;
+        int64_t t = sorted_token[s];
+        double dot = 0.0;
+        for (int64_t c = 0; c < d; ++c) {
+            float g_dy = load_elem(dy, t * d + c, dt);
+            dot += (double)g_dy * (double)load_elem(yp, s * d + c, dt);
+            store_elem(dyp, s * d + c, gate[s] * g_dy, dt);
+        }
+        dgate[s] = (float)dot;
+        if (dlogits) {
+            float g = gate[s];
+            dlogits[t * E + e] = dgate[s] * (g * (1.0f - g));
+        }
+    }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -431,18 +490,24 @@ int64_t oracle_threshold_update(const float* logits, float* thr, int64_t T, int6
     int64_t c = (T * k_target + E - 1) / E;
     if (c < 1) c = 1;
     if (c > T) c = T;
-    uint32_t* keys = (uint32_t*)malloc((size_t)T * sizeof(uint32_t));
-    if (!keys) return -1;
-    for (int64_t e = 0; e < E; ++e) {
-        for (int64_t t = 0; t < T; ++t) {
-            float s = oracle_sigmoid(logits[t * E + e]);
-            keys[t] = (s != s) ? 0u : f2u(s);
+    int failed = 0;
+#pragma omp parallel reduction(| : failed)
+    {
+        uint32_t* keys = (uint32_t*)malloc((size_t)T * sizeof(uint32_t));
+        if (!keys) failed = 1;
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t e = 0; e < E; ++e) {
+            if (!keys) continue;
+            for (int64_t t = 0; t < T; ++t) {
+                float s = oracle_sigmoid(logits[t * E + e]);
+                keys[t] = (s != s) ? 0u : f2u(s);
+            }
+            qsort(keys, (size_t)T, sizeof(uint32_t), cmp_u32_desc);
+            float st = u2f(keys[c - 1]);
+            if (stat) stat[e] = st;
+            thr[e] = fmaf(momentum, thr[e], (1.0f - momentum) * st);
         }
-        qsort(keys, (size_t)T, sizeof(uint32_t), cmp_u32_desc);
-        float st = u2f(keys[c - 1]);
-        if (stat) stat[e] = st;
-        thr[e] = fmaf(momentum, thr[e], (1.0f - momentum) * st);
+        free(keys);
     }
-    free(keys);
-    return c;
+    return failed ? -1 : c;
 }

@@ -94,7 +94,7 @@ __device__ __forceinline__ bool token_span(int T, const int32_t* __restrict__ to
     if (sp.t >= T) return false;
     const int64_t a = tok_off[sp.t];
     const int64_t b = tok_off[sp.t + 1];
-    sp.j0 = (int)min(a, cap);
+    sp.j0 = (int)min(max(a, (int64_t)0), cap);
     sp.j1 = (int)max(min(b, cap), (int64_t)sp.j0);
     return true;
 }
@@ -138,7 +138,7 @@ __device__ __forceinline__ bool piece_span(int t_base, int t_end, uint32_t npiec
     sp.cb = (int64_t)(gw - tl * npieces) * piece_chunks;
     const int64_t a = tok_off[t];
     const int64_t b = tok_off[t + 1];
-    sp.j0 = (int)min(a, cap);
+    sp.j0 = (int)min(max(a, (int64_t)0), cap);      // a list entry below 0 is never read
     sp.j1 = (int)max(min(b, cap), (int64_t)sp.j0);
     return true;
 }
@@ -363,21 +363,42 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
 
 // Vector path, pass 1: one wave per 1 KiB piece of a token's row.
 // For every slot s of the token the wave writes its piece of dYp[s] and the
-// piece's partial dot <dY[t], Yp[s]> (one DPP wave reduction) to
-// part[s * npieces + p].  Yp is read once and dYp written once, both
-// non-temporal.  The wave of piece 0 also zero-fills the token's dlogits row;
-// pass 2 then writes the routed entries.
+// piece's partial dot <dY[t], Yp[s]> to part[s * npieces + p].  The partial
+// is formed in binary64: every product of two binary32 (or bf16) values is
+// exact in binary64, each lane sums its chunk's products in two fma chains
+// (even and odd elements, then added), and the lanes are summed by
+// wave_sum4_rows_f64, so the partial carries about a dozen binary64
+// roundings.  Slots go in batches of four: the four Yp chunks are loaded
+// together, then the four dYp chunks stored, then one reduction serves the
+// four partials.  Yp is read once and dYp written once, both non-temporal.
+// The wave of piece 0 also zero-fills the token's dlogits row; pass 2 then
+// writes the routed entries.
 constexpr int kBwdWaves = 2;
+constexpr int kBwdBatch = 4;
+
+template <int N>
+__device__ __forceinline__ double dot_f64(const double (&dd)[N], const float (&f)[N])
+{
+    double a0 = dd[0] * (double)f[0];
+    double a1 = dd[1] * (double)f[1];
+#pragma unroll
+    for (int i = 2; i < N; i += 2) {
+        a0 = __builtin_fma(dd[i], (double)f[i], a0);
+        a1 = __builtin_fma(dd[i + 1], (double)f[i + 1], a1);
+    }
+    return a0 + a1;
+}
 
 template <int DT>
 __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
     const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate, int t_base,
     int t_end, int64_t nch, uint32_t npieces, const int32_t* __restrict__ tok_off,
     const int32_t* __restrict__ tok_slot, int64_t cap, int E, char* __restrict__ dyp,
-    float* __restrict__ part, float* __restrict__ dlogits)
+    double* __restrict__ part, float* __restrict__ dlogits)
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
+    static_assert(kWave % kBwdBatch == 0 && kBwdBatch == 4, "one wave_sum4_rows_f64 per batch");
     PieceSpan sp;
     if (!piece_span<kBwdWaves>(t_base, t_end, npieces, kWave, tok_off, cap, sp)) return;
     const int lane = lane_id();
@@ -388,57 +409,60 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
     if (dlogits && p == 0)
         for (int e = lane; e < E; e += kWave) dlogits[(int64_t)sp.t * E + e] = 0.0f;
     float df[N];
+    double dd[N];
     {
         v4u w = {0u, 0u, 0u, 0u};
         if (on) w = ld16(dy + (int64_t)sp.t * rb + idx * 16);
         P::unpack(w, df);
+#pragma unroll
+        for (int i = 0; i < N; ++i) dd[i] = (double)df[i];
     }
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
-        const int my = load_slot_block(tok_slot, jb, sp.j1);
+        const int my = load_slot_block(tok_slot, jb, sp.j1);      // -1 past the token's list
         const int n = min(kWave, sp.j1 - jb);
-        // slot walk as in combine_fwd_vec
-        int u = 0;
-        int s = -1;
-        v4u w = {0u, 0u, 0u, 0u};
-        for (; u < n; ++u) {
-            s = __builtin_amdgcn_readlane(my, u);
-            if (s >= 0 && (int64_t)s < cap) break;
-        }
-        if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
-        while (u < n) {
-            const int cur = s;
-            const v4u wc = w;
-            for (++u; u < n; ++u) {
-                s = __builtin_amdgcn_readlane(my, u);
-                if (s >= 0 && (int64_t)s < cap) break;
-            }
-            const float g = gate[cur];
-            float f[N], o[N];
-            P::unpack(wc, f);
-            float acc = 0.0f;
+        for (int u0 = 0; u0 < n; u0 += kBwdBatch) {
+            int sl[kBwdBatch];
+            v4u w[kBwdBatch];
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                acc = __builtin_fmaf(df[i], f[i], acc);
-                o[i] = g * df[i];
+            for (int q = 0; q < kBwdBatch; ++q) {
+                const int s = __builtin_amdgcn_readlane(my, u0 + q);
+                sl[q] = (s >= 0 && (int64_t)s < cap) ? s : -1;
+                w[q] = v4u{0u, 0u, 0u, 0u};
+                if (sl[q] >= 0 && on) w[q] = ld16_nt(yp + (int64_t)sl[q] * rb + idx * 16);
             }
-            if (on) st16_nt(dyp + (int64_t)cur * rb + idx * 16, P::pack(o));
-            const float dot = wave_sum_dpp(acc);
-            if (lane == 0) part[(int64_t)cur * npieces + p] = dot;
-            if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+            double pd[kBwdBatch];
+#pragma unroll
+            for (int q = 0; q < kBwdBatch; ++q) {
+                float f[N];
+                P::unpack(w[q], f);
+                pd[q] = dot_f64<N>(dd, f);
+                if (sl[q] >= 0) {
+                    const float g = gate[sl[q]];
+                    float o[N];
+#pragma unroll
+                    for (int i = 0; i < N; ++i) o[i] = g * df[i];
+                    if (on) st16_nt(dyp + (int64_t)sl[q] * rb + idx * 16, P::pack(o));
+                }
+            }
+            const double dot = wave_sum4_rows_f64(pd[0], pd[1], pd[2], pd[3]);
+            const int r = lane >> 4;
+            const int s = r == 0 ? sl[0] : (r == 1 ? sl[1] : (r == 2 ? sl[2] : sl[3]));
+            if ((lane & 15) == 15 && s >= 0) part[(int64_t)s * npieces + p] = dot;
         }
     }
 }
 
 // Vector path, pass 2: one thread per slot s < min(expert_offsets[E], cap):
-// dgate[s] = the sum of the slot's partial dots in piece order, and
-// dlogits[sorted_token[s], e(s)] = dgate[s] * g (1 - g), with e(s) found by a
-// binary search of expert_offsets in LDS.  A slot that pass 1 skipped (its
+// dgate[s] = the binary64 sum of the slot's partial dots in piece order,
+// rounded once to binary32, and dlogits[sorted_token[s], e(s)] = dgate[s] *
+// (g * (1 - g)) in binary32, with e(s) found by a binary search of
+// expert_offsets in LDS.  A slot that pass 1 skipped (its
 // token-list entry at or past an undersized capacity) gets dgate 0 and leaves
 // its dlogits entry at the zero pass 1 wrote.
 constexpr int kFinishThreads = 256;
 
 __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
-    const float* __restrict__ part, uint32_t npieces, const float* __restrict__ gate,
+    const double* __restrict__ part, uint32_t npieces, const float* __restrict__ gate,
     const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ tok_off,
     const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff, int E, int64_t cap,
     float* __restrict__ dgate, float* __restrict__ dlogits)
@@ -456,7 +480,7 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
         // entry is also below the capacity.  Only the token whose list
         // straddles the capacity needs a search.
         const int t = sorted_token[s];
-        const int64_t a = tok_off[t], b = tok_off[t + 1];
+        const int64_t a = max(tok_off[t], 0), b = tok_off[t + 1];
         bool kept = b <= cap;
         for (int64_t j = a; !kept && j < cap && j < b; ++j) kept = tok_slot[j] == (int32_t)s;
         if (!kept) {
@@ -464,16 +488,17 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
             return;
         }
     }
-    const float* ps = part + s * npieces;
-    float dot = 0.0f;
+    const double* ps = part + s * npieces;
+    double acc = 0.0;
     for (uint32_t q0 = 0; q0 < npieces; q0 += 8) {
-        float v[8];
+        double v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = ps[min(q0 + i, npieces - 1)];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (q0 + i < npieces) dot += v[i];
+            if (q0 + i < npieces) acc += v[i];
     }
+    const float dot = (float)acc;
     dgate[s] = dot;
     if (want_dl) {
         const int e = expert_of_slot(eo, E, (int)s);
@@ -502,13 +527,13 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_elem(
         const int s = tok_slot[j];
         if (s < 0 || (int64_t)s >= cap) continue;
         const float g = gate[s];
-        float part = 0.0f;
+        double part = 0.0;
         for (int64_t c = lane; c < d; c += kWave) {
             const float dv = load_elem<DT>(dy, (int64_t)sp.t * d + c);
-            part = __builtin_fmaf(dv, load_elem<DT>(yp, (int64_t)s * d + c), part);
+            part = __builtin_fma((double)dv, (double)load_elem<DT>(yp, (int64_t)s * d + c), part);
             store_elem<DT>(dyp, (int64_t)s * d + c, g * dv);
         }
-        finish_slot(s, wave_sum(part), g, dgate, eoff_lds, E, want_dl, dlv);
+        finish_slot(s, (float)wave_sum_dpp_f64(part), g, dgate, eoff_lds, E, want_dl, dlv);
     }
     if (want_dl) write_dlogits_row(dlogits, sp.t, E, dlv);
 }
@@ -717,7 +742,7 @@ extern "C" size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slo
     if (!bwd_vector_path(d, dtype)) return 0;
     const int64_t nch = d * elem_bytes(dtype) / 16;
     const int64_t np = (nch + kWave - 1) / kWave;
-    return (size_t)(slot_capacity * np) * sizeof(float);
+    return (size_t)(slot_capacity * np) * sizeof(double);
 }
 
 extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
@@ -745,7 +770,9 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
         if (need > 0 && (!workspace || workspace_bytes < need))
             return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_combine_bwd: workspace needs " + std::to_string(need) +
                                                         " bytes, got " + std::to_string(workspace_bytes));
-        float* part = static_cast<float*>(workspace);
+        if ((reinterpret_cast<uintptr_t>(workspace) & 7) != 0)
+            return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: workspace must be 8-byte aligned");
+        double* part = static_cast<double*>(workspace);
         const int64_t nch = rb / 16;
         const int64_t np = (nch + kWave - 1) / kWave;
         for_each_piece_launch(T, np, kBwdWaves, [&](dim3 grid, int t0, int t1) {

@@ -102,16 +102,19 @@ def test_error_string_is_per_call(et):
 
 def test_combine_bwd_workspace(et):
     lib = et.lib()
-    # one float per slot and 1 KiB piece of the row (C3: d = 4096 bf16 -> 8 pieces)
-    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == 528736 * 8 * 4
-    assert lib.et_combine_bwd_workspace_bytes(4096, 8192, 512, 0) == 8192 * 2 * 4
+    # one binary64 partial per slot and 1 KiB piece of the row (C3: d = 4096 bf16 -> 8 pieces)
+    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == 528736 * 8 * 8
+    assert lib.et_combine_bwd_workspace_bytes(4096, 8192, 512, 0) == 8192 * 2 * 8
     assert lib.et_combine_bwd_workspace_bytes(10, 100, 7, 1) == 0        # element path: none
     assert lib.et_combine_bwd_workspace_bytes(10, 100, 8, 5) == 0        # bad dtype
     p = ctypes.c_void_p(0x1000)                   # 16-byte aligned: the vector path is chosen
     rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, None, 0, None)
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "workspace" in _err(et)
-    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, p, 31, None)
+    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, p, 63, None)
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL
+    odd = ctypes.c_void_p(0x1004)                 # the binary64 partials need 8-byte alignment
+    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, odd, 64, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT and "aligned" in _err(et)
 
 
 def test_router_logits_rejects_bad_arguments(et):

@@ -31,5 +31,5 @@ def test_multi_rank_launch_exits_with_a_message():
 def test_help_lists_the_driver_flags():
     r = _run(["--help"])
     assert r.returncode == 0
-    for flag in ("--gpus", "--steps", "--warmup", "--workload", "--cpu-tokens"):
+    for flag in ("--gpus", "--steps", "--warmup", "--workload", "--cpu-reps", "--no-extras"):
         assert flag in r.stdout

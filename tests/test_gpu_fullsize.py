@@ -5,8 +5,9 @@ through properties that do not need the CPU oracle to touch the rows:
   * dispatch is exactly the row gather Xp = X[sorted_token];
   * combine backward's dYp is exactly bf16(gate * dY[token]) -- one binary32
     multiply and one round-to-nearest-even, which torch's own elementwise ops
-    reproduce -- and dgate matches the float32 row dot within 1e-5 of its
-    absolute mass;
+    reproduce -- and dgate is within one binary32 ulp (2^-23 relative) of
+    the float64 row dot, plus the binary64 summation floor 2 d 2^-53 mass,
+    which implies the specification's 1e-5 relative bar;
   * combine and dispatch backward match a float32 segment-sum reference
     within the bf16 output tolerance (1e-2 relative, plus the float32
     accumulation term), and are bit-identical across two runs (no atomics).
@@ -57,8 +58,11 @@ def test_fullsize_properties(et, orc, dev, name):
     del dyp, want
     ref = (dy_rows.double() * YP.double()).sum(1)
     mass = (dy_rows.double().abs() * YP.double().abs()).sum(1)
-    assert bool(((dgate.double() - ref).abs() <= 1e-5 * mass + 1e-30).all())
-    del dy_rows, ref, mass
+    err = (dgate.double() - ref).abs()
+    rel = float((err / ref.abs().clamp_min(1e-300)).max())
+    print(f"{name}: dgate max_rel={rel:.3g} vs float64", flush=True)
+    assert bool((err <= 2.0 ** -23 * ref.abs() + 2 * d * 2.0 ** -53 * mass).all()), rel
+    del dy_rows, ref, mass, err
 
     k = int(np.diff(r.token_offsets).max())
     for fn, src, w in [(et.combine, YP, gate), (et.dispatch_backward, DXP, None)]:

@@ -1,7 +1,7 @@
 """Seeded random shapes through the whole path on the GPU, against the CPU
 oracle: routing (bit-exact), dispatch, combine and dispatch backward (bit-exact),
-combine backward (dYp bit-exact, dgate and dlogits within 1e-5 of the dot
-mass), the dispatch backward with the router input gradient (bit-exact), and,
+combine backward (dYp bit-exact, dgate within one binary32 ulp of the oracle
+plus the binary64 summation floor, dlogits bit-exact from dgate), the dispatch backward with the router input gradient (bit-exact), and,
 where the shape allows it (bf16, E <= 256, d a multiple of 8), the router
 logits GEMM (exact on integer inputs) and the fused producer + routing
 (bit-identical to router_logits + route).
