@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 7
+#define ET_ABI_VERSION 8
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -99,6 +99,28 @@ int et_route(const float* logits, const float* thr, int64_t num_tokens, int64_t 
              int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
              int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
              int64_t slot_capacity, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Size of the static device scratch of et_route_noalloc (bytes, per GPU). */
+#define ET_ROUTE_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+
+/*
+ * Routing without a workspace argument and without any device allocation:
+ * et_route with its workspace in a static device array of
+ * ET_ROUTE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), for
+ * callers that cannot allocate: code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc.  Arguments and outputs are those of
+ * et_route (bit-identical results); the call runs on the current device, whose
+ * scratch address it looks up once (on its first call there).  Sizes whose
+ * et_route_workspace_bytes(T, E) exceeds the scratch are rejected with
+ * ET_ERR_WORKSPACE_TOO_SMALL: every T fits for E <= 384 (the workspace depends
+ * on E and only weakly on T).  All calls on one GPU share the scratch: calls
+ * that overlap in time on one GPU (different streams or host threads) race.
+ * No counterpart in the reference: an extra entry point of this library.
+ */
+int et_route_noalloc(const float* logits, const float* thr, int64_t num_tokens, int64_t num_experts,
+                     int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                     int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                     int64_t slot_capacity, void* stream);
 
 /*
  * Dispatch (permute / scatter) forward:  Xp[slot, :] = X[token(slot), :].

@@ -45,6 +45,7 @@ _SIGNATURES = {
     "et_last_error": (ctypes.c_char_p, []),
     "et_route_workspace_bytes": (_sz, [_i64, _i64]),
     "et_route": (_int, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _sz, _p]),
+    "et_route_noalloc": (_int, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "et_dispatch_fwd": (_int, [_p, _i64, _i64, _int, _p, _p, _i64, _p, _p]),
     "et_combine_fwd": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _i64, _p, _p]),
     "et_combine_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),

@@ -21,6 +21,7 @@
 //      expert's slots are in token order.  The token-major entry of (t, e) is
 //      the token's offset plus the number of selected experts below e.
 #include <algorithm>
+#include <mutex>
 
 #include "et_common.hpp"
 #include "et_route_internal.hpp"
@@ -521,23 +522,37 @@ extern "C" size_t et_route_workspace_bytes(int64_t num_tokens, int64_t num_exper
     return route_ws_layout(nullptr, route_plan(num_tokens, num_experts), num_experts).bytes;
 }
 
+// Argument checks shared by et_route and et_route_noalloc (no HIP call).
+static int route_check(const char* fn, const float* logits, const float* thr, int64_t T, int64_t E,
+                       const int32_t* counts, const int32_t* expert_offsets, const int32_t* token_offsets,
+                       const int32_t* sorted_token, const float* slot_gate, const int32_t* token_slot,
+                       int64_t slot_capacity)
+{
+    const std::string f(fn);
+    if (T < 0) return fail(ET_ERR_INVALID_ARGUMENT, f + ": num_tokens < 0");
+    if (E < 1 || E > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, f + ": num_experts must be in [1, " +
+                                                 std::to_string(ET_MAX_EXPERTS) + "]");
+    if (T * E >= (int64_t(1) << 31))
+        return fail(ET_ERR_INVALID_ARGUMENT, f + ": num_tokens * num_experts must be < 2^31");
+    if (slot_capacity < 0) return fail(ET_ERR_INVALID_ARGUMENT, f + ": slot_capacity < 0");
+    if (!thr || !counts || !expert_offsets || !token_offsets)
+        return fail(ET_ERR_INVALID_ARGUMENT, f + ": null thr/counts/offsets pointer");
+    if (T > 0 && !logits) return fail(ET_ERR_INVALID_ARGUMENT, f + ": null logits");
+    if (slot_capacity > 0 && (!sorted_token || !slot_gate || !token_slot))
+        return fail(ET_ERR_INVALID_ARGUMENT, f + ": null slot array with slot_capacity > 0");
+    return ET_OK;
+}
+
 extern "C" int et_route(const float* logits, const float* thr, int64_t T, int64_t E,
                         int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
                         int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
                         int64_t slot_capacity, void* workspace, size_t workspace_bytes, void* stream)
 {
-    if (T < 0) return fail(ET_ERR_INVALID_ARGUMENT, "et_route: num_tokens < 0");
-    if (E < 1 || E > ET_MAX_EXPERTS)
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_route: num_experts must be in [1, " +
-                                                 std::to_string(ET_MAX_EXPERTS) + "]");
-    if (T * E >= (int64_t(1) << 31))
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_route: num_tokens * num_experts must be < 2^31");
-    if (slot_capacity < 0) return fail(ET_ERR_INVALID_ARGUMENT, "et_route: slot_capacity < 0");
-    if (!thr || !counts || !expert_offsets || !token_offsets || !workspace)
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_route: null thr/counts/offsets/workspace pointer");
-    if (T > 0 && !logits) return fail(ET_ERR_INVALID_ARGUMENT, "et_route: null logits");
-    if (slot_capacity > 0 && (!sorted_token || !slot_gate || !token_slot))
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_route: null slot array with slot_capacity > 0");
+    if (int rc = route_check("et_route", logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token,
+                             slot_gate, token_slot, slot_capacity))
+        return rc;
+    if (!workspace) return fail(ET_ERR_INVALID_ARGUMENT, "et_route: null workspace pointer");
     const RoutePlan p = route_plan(T, E);
     const RouteWs ws = route_ws_layout(workspace, p, E);
     if (workspace_bytes < ws.bytes)
@@ -561,4 +576,73 @@ extern "C" int et_route(const float* logits, const float* thr, int64_t T, int64_
                               ws.block_slot_base, expert_offsets, token_offsets, sorted_token, slot_gate,
                               token_slot, slot_capacity));
     return check_launch("route_fill_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// et_route_noalloc: et_route with its workspace in a static device array
+// ---------------------------------------------------------------------------
+//
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops that forbid hipMalloc).  The routing kernels' block
+// and wave counts live in `scratch`, one copy per GPU for the life of the
+// process.  Its address is taken once per device with hipGetSymbolAddress
+// (on the first call with that device current) and kept in g_scratch; the
+// kernels receive that device address, never the host-side symbol.  Every
+// region of the workspace is written by the count kernel before the scan and
+// fill kernels read it, so nothing needs clearing between calls.  All calls
+// on one GPU share the array: calls that overlap in time on one GPU (on
+// different streams, or from different host threads) race.
+
+namespace et {
+
+constexpr size_t kRouteScratchBytes = ET_ROUTE_NOALLOC_SCRATCH_BYTES;
+constexpr int kScratchDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kRouteScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch[kScratchDevices] = {};
+
+// Device address of the current device's copy of `scratch`.
+static int route_scratch(void** out)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(ET_ERR_LAUNCH, std::string("et_route_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kScratchDevices)
+        return fail(ET_ERR_UNSUPPORTED, "et_route_noalloc: device index " + std::to_string(dev) + " beyond " +
+                                            std::to_string(kScratchDevices));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(ET_ERR_LAUNCH, std::string("et_route_noalloc: hipGetSymbolAddress(scratch): ") +
+                                           hipGetErrorString(e));
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return ET_OK;
+}
+
+}  // namespace et
+
+extern "C" int et_route_noalloc(const float* logits, const float* thr, int64_t T, int64_t E,
+                                int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                                int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                                int64_t slot_capacity, void* stream)
+{
+    if (int rc = route_check("et_route_noalloc", logits, thr, T, E, counts, expert_offsets, token_offsets,
+                             sorted_token, slot_gate, token_slot, slot_capacity))
+        return rc;
+    const size_t need = route_ws_layout(nullptr, route_plan(T, E), E).bytes;
+    if (need > kRouteScratchBytes)
+        return fail(ET_ERR_WORKSPACE_TOO_SMALL,
+                    "et_route_noalloc: T=" + std::to_string(T) + ", E=" + std::to_string(E) + " needs " +
+                        std::to_string(need) + " bytes of scratch; the static scratch holds " +
+                        std::to_string(kRouteScratchBytes) + " (call et_route with a workspace)");
+    void* ws = nullptr;
+    if (int rc = route_scratch(&ws)) return rc;
+    return et_route(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
+                    slot_capacity, ws, kRouteScratchBytes, stream);
 }

@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 24
+    assert len(syms) == 25
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name
@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 7" in hdr
-    assert et.lib().et_abi_version() == 7
+    assert "#define ET_ABI_VERSION 8" in hdr
+    assert et.lib().et_abi_version() == 8
 
 
 def test_workspace_sizes(et):
@@ -58,6 +58,25 @@ def test_route_rejects_bad_arguments_without_launching(et):
     assert rc == ET_ERR_INVALID_ARGUMENT
     rc = lib.et_route(dummy, dummy, 4096, 8, dummy, dummy, dummy, dummy, dummy, dummy, 16, ws, 16, None)
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "workspace" in _err(et)
+
+
+def test_route_noalloc_rejects_bad_arguments_and_oversize_without_launching(et):
+    """The no-allocation routing checks its arguments, then whether the
+    workspace et_route would need fits the static scratch (8 MiB: every T up
+    to E = 408), all before any HIP call."""
+    lib = et.lib()
+    d = ctypes.c_void_p(0x2000)
+    rc = lib.et_route_noalloc(d, d, 16, 0, d, d, d, d, d, d, 16, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT and "et_route_noalloc" in _err(et) and "num_experts" in _err(et)
+    rc = lib.et_route_noalloc(None, d, 16, 4, d, d, d, d, d, d, 16, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT and "logits" in _err(et)
+    rc = lib.et_route_noalloc(d, d, 16, 4, d, d, d, None, d, d, 16, None)
+    assert rc == ET_ERR_INVALID_ARGUMENT
+    # E = 1024 at T = 65536 needs ~21 MB of workspace: rejected, with the sizes named
+    assert lib.et_route_workspace_bytes(65536, 1024) > 8 << 20
+    rc = lib.et_route_noalloc(d, d, 65536, 1024, d, d, d, d, d, d, 16, None)
+    assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "scratch" in _err(et) and str(8 << 20) in _err(et)
+    assert lib.et_route_workspace_bytes(65536, 408) <= 8 << 20 < lib.et_route_workspace_bytes(65536, 409)
 
 
 def test_row_entry_points_reject_bad_arguments(et):
