@@ -2,9 +2,11 @@
 
 Import with ``importlib.import_module("peer-review-agents_amd")`` (the
 directory name is not a Python identifier).  Kernels live in csrc/ and are
-built into libetmoe.so by build.py; the host API is in expert_threshold.py.
+built into libetmoe.so by build.py; the host API is in expert_threshold.py,
+and ops.py registers the path as PyTorch operators (torch.ops.etmoe.*).
 """
 from ._lib import ETMoEError, LIB_PATH, header_symbols, lib  # noqa: F401
+from . import ops  # noqa: F401  (registers torch.ops.etmoe.*)
 from .expert_threshold import (  # noqa: F401
     ExpertThresholdRouter,
     RoutingPlan,

@@ -116,7 +116,7 @@ class RoutingPlan:
 
     @property
     def device(self) -> torch.device:
-        return self.expert_offsets.device
+        return self.token_offsets.device
 
 
 def route_workspace_bytes(num_tokens: int, num_experts: int) -> int:
@@ -164,13 +164,19 @@ def route(logits: torch.Tensor, thr: torch.Tensor, *, slot_capacity: Optional[in
     check("et_route", rc)
     plan = RoutingPlan(counts, eo, to, st, sg, ts, T, E, cap)
     if sync:
-        S = int(eo[E].item())
-        plan.num_slots = S
-        plan.sorted_token = st[:S]
-        plan.slot_gate = sg[:S]
-        plan.token_slot = ts[:S]
-        plan.capacity = S
+        _shrink(plan, int(eo[E].item()))
     return plan
+
+
+def _shrink(plan: RoutingPlan, S: int) -> None:
+    """Exactly-sized copies of the slot arrays of a plan routed at capacity
+    T*E, so the T*E buffers are released (a plan held until a backward pass
+    then pins 12 bytes per slot, not per token-expert pair)."""
+    plan.num_slots = S
+    plan.sorted_token = plan.sorted_token[:S].clone()
+    plan.slot_gate = plan.slot_gate[:S].clone()
+    plan.token_slot = plan.token_slot[:S].clone()
+    plan.capacity = S
 
 
 # --------------------------------------------------------------------------- #
@@ -691,12 +697,7 @@ def router_route(x: torch.Tensor, w: torch.Tensor, thr: torch.Tensor, *, slot_ca
     check("et_router_route", rc)
     plan = RoutingPlan(counts, eo, to, st, sg, ts, T, E, cap)
     if sync:
-        S = int(eo[E].item())
-        plan.num_slots = S
-        plan.sorted_token = st[:S]
-        plan.slot_gate = sg[:S]
-        plan.token_slot = ts[:S]
-        plan.capacity = S
+        _shrink(plan, int(eo[E].item()))
     return (plan, L) if want_logits else plan
 
 
