@@ -448,10 +448,25 @@ def expert_gemm_fp8(a: torch.Tensor, a_scale: torch.Tensor, w: torch.Tensor, w_s
     epi = {"none": ET_GEMM_PLAIN, "swiglu": ET_GEMM_SWIGLU}.get(epilogue)
     if epi is None:
         raise ValueError(f"unknown epilogue {epilogue!r} (the fp8 GEMM has 'none' and 'swiglu')")
-    if not gather and a.shape[0] != plan.rows:
+    if K < 16 or K % 16 or K >= 1 << 22:
+        raise ValueError(f"K must be a positive multiple of 16 below 2^22, got {K}")
+    if N < 8 or N % 8 or (epi == ET_GEMM_SWIGLU and N % 16):
+        raise ValueError(f"N must be a positive multiple of 8 (16 for swiglu), got {N}")
+    if N * K >= 1 << 31:
+        raise ValueError("one expert's weight must be below 2 GiB")
+    if gather:
+        if a.shape[0] != plan.num_tokens:
+            raise ValueError(f"a has {a.shape[0]} rows, plan has {plan.num_tokens} tokens")
+        if a.shape[0] * K >= 1 << 31:
+            raise ValueError("in gather mode the token matrix must be below 2 GiB")
+    elif a.shape[0] != plan.rows:
         raise ValueError(f"slot-major a must have {plan.rows} rows")
     ncol = N // 2 if epi == ET_GEMM_SWIGLU else N
     c = _out_or_new(out, (plan.rows, ncol), torch.bfloat16, dev, "out")
+    if a.data_ptr() % 16 or w.data_ptr() % 16 or c.data_ptr() % 16:
+        raise ValueError("a, w and out must be 16-byte aligned")
+    if a_scale.data_ptr() % 4 or w_scale.data_ptr() % 4:
+        raise ValueError("a_scale and w_scale must be 4-byte aligned")
     with torch.cuda.device(dev):
         rc = lib().et_expert_gemm_fp8(_vp(a), a.shape[0], _vp(a_scale), _vp(plan.sorted_token) if gather else None,
                                       _vp(w), _vp(w_scale), _vp(plan.expert_offsets), E, K, N, plan.rows, epi,

@@ -50,3 +50,35 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(lib_mod, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         lib_mod.lib()
+
+
+def test_expert_gemm_fp8_checks_shapes_like_bf16(et):
+    """The fp8 grouped GEMM validates what the bf16 one does, in Python and
+    before any device call (fake HIP tensors: shapes only): a gather operand
+    shorter than the token count, K off the 16-element step, N off the
+    8-element step (16 for SwiGLU)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    f8 = torch.float8_e4m3fn
+    with FakeTensorMode():
+        T, E, K, N = 64, 4, 128, 64
+        i32 = dict(dtype=torch.int32, device="cuda")
+        plan = et.RoutingPlan(torch.empty(E, **i32), torch.empty(E + 1, **i32), torch.empty(T + 1, **i32),
+                              torch.empty(100, **i32), torch.empty(100, device="cuda"), torch.empty(100, **i32),
+                              T, E, 100, 100)
+
+        def call(a_rows=T, k=K, n=N, epilogue="none", gather=True):
+            a = torch.empty(a_rows, k, dtype=f8, device="cuda")
+            w = torch.empty(E, n, k, dtype=f8, device="cuda")
+            return et.expert_gemm_fp8(a, torch.empty(a_rows, device="cuda"), w, torch.empty(E, n, device="cuda"),
+                                      plan, gather=gather, epilogue=epilogue)
+
+        with pytest.raises(ValueError, match="tokens"):
+            call(a_rows=T - 1)
+        with pytest.raises(ValueError, match="K must"):
+            call(k=120)
+        with pytest.raises(ValueError, match="N must"):
+            call(n=60)
+        with pytest.raises(ValueError, match="N must"):
+            call(n=72, epilogue="swiglu")
+        with pytest.raises(ValueError, match="slot-major"):
+            call(a_rows=99, gather=False)
