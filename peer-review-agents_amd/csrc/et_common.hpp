@@ -176,51 +176,6 @@ __device__ __forceinline__ double wave_sum_dpp_f64(double v)
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-// Lane exchanges of gfx950: v_permlane32_swap exchanges lanes 32..63 of its
-// first operand with lanes 0..31 of its second; v_permlane16_swap exchanges
-// the odd 16-lane rows of its first operand with the even rows of its second.
-// Each returns (first, second) after the exchange; a double moves as two words.
-__device__ __forceinline__ void permlane32_swap_f64(double& a, double& b)
-{
-    uint64_t ua = __builtin_bit_cast(uint64_t, a), ub = __builtin_bit_cast(uint64_t, b);
-    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)ua, (uint32_t)ub, false, false);
-    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(ua >> 32), (uint32_t)(ub >> 32), false, false);
-    a = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
-    b = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
-}
-
-__device__ __forceinline__ void permlane16_swap_f64(double& a, double& b)
-{
-    uint64_t ua = __builtin_bit_cast(uint64_t, a), ub = __builtin_bit_cast(uint64_t, b);
-    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)ua, (uint32_t)ub, false, false);
-    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(ua >> 32), (uint32_t)(ub >> 32), false, false);
-    a = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
-    b = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
-}
-
-// Wave sums of four binary64 values per lane, one per 16-lane row: lane
-// 16 r + 15 returns the sum over all 64 lanes of v_r (other lanes return
-// partial sums).  Step 1 pairs (v0, v2) and (v1, v3) across the wave halves
-// (lane l adds lane l ^ 32): the low half then holds v0 / v1, the high half
-// v2 / v3.  Step 2 pairs the two results across adjacent rows, leaving row r
-// with 16 partial sums of v_r.  A DPP tree (pairs, quads, row_shr 4 and 8)
-// then sums each row into its lane 15.  The order of the additions is fixed,
-// and four slots cost about as much as one full wave reduction.
-__device__ __forceinline__ double wave_sum4_rows_f64(double v0, double v1, double v2, double v3)
-{
-    permlane32_swap_f64(v0, v2);
-    permlane32_swap_f64(v1, v3);
-    double a = v0 + v2;          // low half: v0(l) + v0(l + 32); high half: v2(l - 32) + v2(l)
-    double b = v1 + v3;
-    permlane16_swap_f64(a, b);
-    double c = a + b;            // row 0: v0, row 1: v1, row 2: v2, row 3: v3
-    c += dpp_mov_f64<0xB1>(c);   // quad_perm [1,0,3,2]
-    c += dpp_mov_f64<0x4E>(c);   // quad_perm [2,3,0,1]
-    c += dpp_mov_f64<0x114>(c);  // row_shr:4
-    c += dpp_mov_f64<0x118>(c);  // row_shr:8
-    return c;
-}
-
 // Max over the wave's 64 lanes of an unsigned key, with the DPP moves of
 // wave_sum_dpp (lanes outside a move's source row take 0, the identity of an
 // unsigned max).  Returned wave-uniform.

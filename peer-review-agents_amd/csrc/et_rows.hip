@@ -366,15 +366,17 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
 // piece's partial dot <dY[t], Yp[s]> to part[s * npieces + p].  The partial
 // is formed in binary64: every product of two binary32 (or bf16) values is
 // exact in binary64, each lane sums its chunk's products in two fma chains
-// (even and odd elements, then added), and the lanes are summed by
-// wave_sum4_rows_f64, so the partial carries about a dozen binary64
-// roundings.  Slots go in batches of four: the four Yp chunks are loaded
-// together, then the four dYp chunks stored, then one reduction serves the
-// four partials.  Yp is read once and dYp written once, both non-temporal.
-// The wave of piece 0 also zero-fills the token's dlogits row; pass 2 then
-// writes the routed entries.
+// (even and odd elements, then added), and one DPP wave reduction sums the
+// lanes, so the partial carries about a dozen binary64 roundings.  Yp is read
+// once and dYp written once, both non-temporal.  The slot walk is that of
+// combine_fwd_vec: the next slot's chunk is loaded after the current slot's
+// store, so one load and one store are in flight per wave.  (Batching four
+// slots' loads ahead of their stores, with one reduction for the four, was
+// 1-9% slower across routing shapes, with or without the arithmetic: the
+// access order, not the binary64 work, sets the time.)  The wave of piece 0
+// also zero-fills the token's dlogits row; pass 2 then writes the routed
+// entries.
 constexpr int kBwdWaves = 2;
-constexpr int kBwdBatch = 4;
 
 template <int N>
 __device__ __forceinline__ double dot_f64(const double (&dd)[N], const float (&f)[N])
@@ -398,7 +400,6 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
-    static_assert(kWave % kBwdBatch == 0 && kBwdBatch == 4, "one wave_sum4_rows_f64 per batch");
     PieceSpan sp;
     if (!piece_span<kBwdWaves>(t_base, t_end, npieces, kWave, tok_off, cap, sp)) return;
     const int lane = lane_id();
@@ -418,36 +419,33 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
         for (int i = 0; i < N; ++i) dd[i] = (double)df[i];
     }
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
-        const int my = load_slot_block(tok_slot, jb, sp.j1);      // -1 past the token's list
+        const int my = load_slot_block(tok_slot, jb, sp.j1);
         const int n = min(kWave, sp.j1 - jb);
-        for (int u0 = 0; u0 < n; u0 += kBwdBatch) {
-            int sl[kBwdBatch];
-            v4u w[kBwdBatch];
-#pragma unroll
-            for (int q = 0; q < kBwdBatch; ++q) {
-                const int s = __builtin_amdgcn_readlane(my, u0 + q);
-                sl[q] = (s >= 0 && (int64_t)s < cap) ? s : -1;
-                w[q] = v4u{0u, 0u, 0u, 0u};
-                if (sl[q] >= 0 && on) w[q] = ld16_nt(yp + (int64_t)sl[q] * rb + idx * 16);
+        // slot walk as in combine_fwd_vec
+        int u = 0;
+        int s = -1;
+        v4u w = {0u, 0u, 0u, 0u};
+        for (; u < n; ++u) {
+            s = __builtin_amdgcn_readlane(my, u);
+            if (s >= 0 && (int64_t)s < cap) break;
+        }
+        if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+        while (u < n) {
+            const int cur = s;
+            const v4u wc = w;
+            for (++u; u < n; ++u) {
+                s = __builtin_amdgcn_readlane(my, u);
+                if (s >= 0 && (int64_t)s < cap) break;
             }
-            double pd[kBwdBatch];
+            const float g = gate[cur];
+            float f[N], o[N];
+            P::unpack(wc, f);
 #pragma unroll
-            for (int q = 0; q < kBwdBatch; ++q) {
-                float f[N];
-                P::unpack(w[q], f);
-                pd[q] = dot_f64<N>(dd, f);
-                if (sl[q] >= 0) {
-                    const float g = gate[sl[q]];
-                    float o[N];
-#pragma unroll
-                    for (int i = 0; i < N; ++i) o[i] = g * df[i];
-                    if (on) st16_nt(dyp + (int64_t)sl[q] * rb + idx * 16, P::pack(o));
-                }
-            }
-            const double dot = wave_sum4_rows_f64(pd[0], pd[1], pd[2], pd[3]);
-            const int r = lane >> 4;
-            const int s = r == 0 ? sl[0] : (r == 1 ? sl[1] : (r == 2 ? sl[2] : sl[3]));
-            if ((lane & 15) == 15 && s >= 0) part[(int64_t)s * npieces + p] = dot;
+            for (int i = 0; i < N; ++i) o[i] = g * df[i];
+            if (on) st16_nt(dyp + (int64_t)cur * rb + idx * 16, P::pack(o));
+            const double dot = wave_sum_dpp_f64(dot_f64<N>(dd, f));
+            if (lane == 0) part[(int64_t)cur * npieces + p] = dot;
+            if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
         }
     }
 }
