@@ -612,14 +612,63 @@ class Step:
             setattr(self, name, None)
 
 
-def extra_workload(et, lib, dev, workload: str, seed: int, stages, steps: int = 10, warmup: int = 3) -> dict:
+def expert_gemm_brief(et, dev, stream, plan, X, reps: int = 3) -> dict:
+    """The expert FFN's two projections on a workload's routing (gate/up with
+    the dispatch fused, down slot-major), each against torch's grouped GEMM
+    (hipBLASLt) plus, for gate/up, the dispatch torch needs.  Random-init
+    weights of the FFN shape of the headline leg."""
+    import torch
+    T, d = X.shape
+    E, S, F = plan.num_experts, plan.rows, EXPERT_FFN
+    g = torch.Generator(device=dev)
+    g.manual_seed(4245)
+    w1 = (torch.randn(E, 2 * F, d, device=dev, generator=g) * d ** -0.5).to(torch.bfloat16)
+    w2 = (torch.randn(E, d, F, device=dev, generator=g) * F ** -0.5).to(torch.bfloat16)
+    h = torch.empty(S, 2 * F, dtype=torch.bfloat16, device=dev)
+    a2 = torch.randn(S, F, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(S, d, dtype=torch.bfloat16, device=dev)
+    xp = et.dispatch(X, plan)
+    offs = plan.expert_offsets[1:].contiguous()
+
+    def timed(fn):
+        fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    t_up = timed(lambda: et.expert_gemm(X, w1, plan, out=h))
+    t_down = timed(lambda: et.expert_gemm(a2, w2, plan, gather=False, out=y))
+    t_disp = timed(lambda: et.dispatch(X, plan, out=xp))
+    w1t, w2t = w1.transpose(1, 2), w2.transpose(1, 2)
+    t_up_lib = timed(lambda: torch._grouped_mm(xp, w1t, offs=offs))
+    t_down_lib = timed(lambda: torch._grouped_mm(a2, w2t, offs=offs))
+    fl_up, fl_down = 2.0 * S * d * 2 * F, 2.0 * S * F * d
+    del w1, w2, h, a2, y, xp
+    return {"expert_ffn": F,
+            "gate_up_ms": round(t_up, 3), "gate_up_frac": round(fl_up / (t_up * 1e-3) / MFMA_BF16_PEAK, 4),
+            "torch_grouped_mm_gate_up_ms": round(t_up_lib, 3), "dispatch_ms": round(t_disp, 3),
+            "down_ms": round(t_down, 3), "down_frac": round(fl_down / (t_down * 1e-3) / MFMA_BF16_PEAK, 4),
+            "torch_grouped_mm_down_ms": round(t_down_lib, 3)}
+
+
+def extra_workload(et, lib, dev, workload: str, seed: int, stages, steps: int = 10, warmup: int = 3,
+                   gemm: bool = False) -> dict:
     """A full-size step of another configuration, timed like the headline
-    step (HIP events per stage, wall clock per step), its buffers freed after."""
+    step (HIP events per stage, wall clock per step), its buffers freed after.
+    With `gemm`, the expert FFN projections on its routing too."""
     import torch
     st = Step(et, lib, dev, workload, seed)
     stage_ms, wall_ms = st.timed(steps, warmup, stages)
     out = st.summary(stages, stage_ms, wall_ms)
     out["steps"] = steps
+    if gemm and st.act == torch.bfloat16:
+        plan = et.RoutingPlan(st.counts, st.eoff, st.toff, st.st, st.sg, st.ts, st.T, st.E, st.S, st.S)
+        out["expert_gemm"] = expert_gemm_brief(et, dev, st.stream, plan, st.X)
     st.release()
     del st
     torch.cuda.empty_cache()
@@ -760,11 +809,16 @@ def main() -> int:
         for name, stages in (("C2", all_stages), ("C4", [3, 4])):
             if name == args.workload:
                 continue
-            extras[name] = extra_workload(et, lib, dev, name, args.seed, stages)
+            extras[name] = extra_workload(et, lib, dev, name, args.seed, stages, gemm=True)
             x = extras[name]
             print(f"  {name} full size ({'+'.join(x['stages'])}): {x['ms_per_step']:.4f} ms per step, "
                   f"{x['slots_per_s'] / 1e6:.2f} M slots/s, {100 * x['hbm_frac']:.1f}% of HBM peak, mean k "
                   f"{x['mean_k']}", file=sys.stderr, flush=True)
+            if "expert_gemm" in x:
+                b = x["expert_gemm"]
+                print(f"    expert GEMM: gate/up {b['gate_up_ms']:.3f} ms (torch grouped {b['torch_grouped_mm_gate_up_ms']:.3f}"
+                      f" + dispatch {b['dispatch_ms']:.3f}), down {b['down_ms']:.3f} ms (torch grouped "
+                      f"{b['torch_grouped_mm_down_ms']:.3f})", file=sys.stderr, flush=True)
 
     cpu = None
     if args.cpu_reps > 0:

@@ -43,9 +43,9 @@
 // CU).  Each block computes the per-expert tile prefix once, then walks its
 // tiles.  The 8 XCDs take blocks in turn (block b runs on XCD b % 8), so XCD
 // x is given the contiguous range of tiles [x * per, (x + 1) * per); inside an
-// expert, tiles are ordered in groups of 4 slot tiles x every feature tile, so
-// the ~32 blocks running together on one XCD share 4 A tiles and 8 W tiles
-// through that XCD's L2 (the larger A is fetched again less often; an
+// expert, tiles are ordered in groups of 4 or 8 slot tiles x every feature
+// tile, so the ~32 blocks running together on one XCD share a few A tiles and
+// W tiles through that XCD's L2 (the larger A is fetched again less often; an
 // expert's W is re-read from the last-level cache).  A block's tiles form one stream of chunks: the last
 // two chunks of a tile load the next tile's first two, so the ~6 us a tile
 // otherwise spent filling its pipeline and storing its output overlaps the
@@ -78,7 +78,11 @@ constexpr int kBM = 256;          // slots per tile
 constexpr int kBN = 256;          // output features per tile
 constexpr int kKC = 64;           // k per chunk (four k-steps of 16): 128 bytes of a row
 constexpr int kThreads = 256;
-constexpr int kGroupM = 4;        // slot tiles per group in the tile order
+// Slot tiles per group in the tile order: 8 for K >= 2048 (the gate/up
+// projections: 2.5-3% faster than 4 at C3 and C4), 4 below (the down
+// projection: 4.6% faster than 8 at C3).  The order changes no bits.
+constexpr int kGroupMLargeK = 8;
+constexpr int kGroupMSmallK = 4;
 constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
 constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
 constexpr int kSmemBytes = 2 * kStage;
@@ -217,6 +221,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int nN = EPI == EPI_SWIGLU ? (F + kBN / 2 - 1) / (kBN / 2) : (N + kBN - 1) / kBN;
     const int Q = ptile[E] * nN;
     const int per = (Q + 7) / 8;
+    const int group_m = K >= 2048 ? kGroupMLargeK : kGroupMSmallK;
     const int nloc = (int)(gridDim.x / 8);
     const int xcd = (int)(blockIdx.x & 7);
     const int r32 = lane & 31;
@@ -270,10 +275,10 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int e = lo;
         const int mte = ptile[e + 1] - ptile[e];
         const int qq = q - ptile[e] * nN;
-        const int grp = qq / (kGroupM * nN);
-        const int gm = min(kGroupM, mte - grp * kGroupM);
-        const int idx = qq - grp * kGroupM * nN;
-        const int mt = grp * kGroupM + idx % gm;
+        const int grp = qq / (group_m * nN);
+        const int gm = min(group_m, mte - grp * group_m);
+        const int idx = qq - grp * group_m * nN;
+        const int mt = grp * group_m + idx % gm;
         const int nt = idx / gm;
         t.s0 = (int64_t)g.expert_offsets[e] + (int64_t)mt * kBM;
         const int64_t rend = min<int64_t>(g.expert_offsets[e + 1], g.cap);
