@@ -115,20 +115,21 @@ def threshold_dynamics(et, W, dev, stream, workload: str, seed: int) -> dict:
     stat = torch.empty(E, dtype=torch.float32, device=dev)
     plan = et.route(logits[0], thr, slot_capacity=cap, workspace=rws)       # warm-up
     et.threshold_update_(thr.clone(), logits[0], cfg["k_target"], cfg["momentum"], stat=stat, workspace=tws)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    r_ms = u_ms = 0.0
+    # Events on the stream, no host synchronisation inside the loop (the host
+    # runs ahead, so each interval is the kernels' own time on the GPU).
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     slots = []
     for i in range(steps):
-        ev[0].record(stream)
+        ev[i][0].record(stream)
         plan = et.route(logits[i], thr, slot_capacity=cap, workspace=rws)
-        ev[1].record(stream)
+        ev[i][1].record(stream)
         et.threshold_update_(thr, logits[i], cfg["k_target"], cfg["momentum"], stat=stat, workspace=tws)
-        ev[2].record(stream)
+        ev[i][2].record(stream)
         slots.append(plan.expert_offsets[E:E + 1])
-        torch.cuda.synchronize()
-        r_ms += ev[0].elapsed_time(ev[1])
-        u_ms += ev[1].elapsed_time(ev[2])
+    torch.cuda.synchronize()
+    r_ms = sum(e[0].elapsed_time(e[1]) for e in ev)
+    u_ms = sum(e[1].elapsed_time(e[2]) for e in ev)
     k = [int(x) / T for x in slots]
     thr_eager = thr.clone()
     # All steps captured in one HIP graph and replayed once from the start
@@ -804,9 +805,10 @@ def main() -> int:
             print(f"  SwiGLU for training: forward {sw['forward_ms']:.3f} ms ({100 * sw['forward_frac']:.1f}% of peak), "
                   f"backward {sw['backward_ms']:.3f} ms ({100 * sw['backward_frac']:.1f}% of peak)", file=sys.stderr,
                   flush=True)
-        # the other row configurations at full size: C2 (variable k, all five
+        # the other row configurations at full size: C1 (the CPU reference
+        # configuration, f32, all five stages), C2 (variable k, all five
         # stages) and C4 (one GPU's EP=8 expert share, backward only)
-        for name, stages in (("C2", all_stages), ("C4", [3, 4])):
+        for name, stages in (("C1", all_stages), ("C2", all_stages), ("C4", [3, 4])):
             if name == args.workload:
                 continue
             extras[name] = extra_workload(et, lib, dev, name, args.seed, stages, gemm=True)

@@ -96,3 +96,31 @@ def test_threshold_dynamics_c5_full_size(et, orc, dev):
         thr_o, stat_o = orc.threshold_update(lg, thr_o, cfg["k_target"], cfg["momentum"])
         np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
         np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
+
+
+def test_threshold_dynamics_c5_full_size_100_steps(et, orc, dev):
+    """C5 as configured: 100 routing steps at T = 131072, E = 64, each on fresh
+    logits (drawn on the device, then copied to the host for the oracle) and
+    followed by the EMA update from thr0 = 0.95.  The statistic and the
+    thresholds are bit-exact with the oracle after every step, and the
+    routing is bit-exact at every 10th step (and the first and last)."""
+    from test_gpu_parity import assert_route_equal, bits
+
+    cfg = W.CONFIGS["C5"]
+    T, E, k, m = cfg["T"], cfg["E"], cfg["k_target"], cfg["momentum"]
+    thr_o = np.full(E, cfg["thr0"], np.float32)
+    thr = dev_f32(thr_o, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    for step in range(cfg["steps"]):
+        L = torch.randn(T, E, device=dev, generator=g)
+        lg = host(L)
+        if step % 10 == 0 or step == cfg["steps"] - 1:
+            print(f"C5 100-step dynamics: step {step}", flush=True)
+            assert_route_equal(et.route(L, thr), orc.route(lg, thr_o))
+        stat = et.threshold_update_(thr, L, k, m)
+        thr_o, stat_o = orc.threshold_update(lg, thr_o, k, m)
+        np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+        np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
+    # the EMA moved the thresholds down from 0.95 towards the k_target statistic
+    assert float(thr_o.max()) < cfg["thr0"]
