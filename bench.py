@@ -687,6 +687,8 @@ def main() -> int:
                     help="timed passes of the CPU baseline after its warm-up (0 skips it)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the side measurements (other configs, router, expert GEMM)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the full-size steps of the other configurations (C1, C2, C4)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -809,7 +811,7 @@ def main() -> int:
         # configuration, f32, all five stages), C2 (variable k, all five
         # stages) and C4 (one GPU's EP=8 expert share, backward only)
         for name, stages in (("C1", all_stages), ("C2", all_stages), ("C4", [3, 4])):
-            if name == args.workload:
+            if name == args.workload or args.no_other_configs:
                 continue
             extras[name] = extra_workload(et, lib, dev, name, args.seed, stages, gemm=True)
             x = extras[name]
