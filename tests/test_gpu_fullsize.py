@@ -124,3 +124,54 @@ def test_threshold_dynamics_c5_full_size_100_steps(et, orc, dev):
         np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
     # the EMA moved the thresholds down from 0.95 towards the k_target statistic
     assert float(thr_o.max()) < cfg["thr0"]
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+def test_rows_full_size_against_oracle(et, orc, dev, name):
+    """Every configuration at its full size against the CPU oracle itself
+    (C, threaded; the same bits for any thread count): routing, dispatch,
+    combine, combine backward with dlogits and dispatch backward on the same
+    inputs (drawn on the device, copied to the host).  Bit-exact, except dgate:
+    within one binary32 ulp plus the binary64 summation floor.  C5's rows are
+    routed at its EMA start thresholds (nearly every token on the fallback)."""
+    from test_gpu_parity import assert_dgate, assert_dlogits, assert_route_equal, bits
+
+    cfg = W.CONFIGS[name]
+    T, d, E = cfg["T"], cfg["d"], cfg["E"]
+    lg, thr = W.router_inputs(name, seed=0)
+    L, TH = dev_f32(lg, dev), dev_f32(thr, dev)
+    plan = et.route(L, TH)
+    r = orc.route(lg, thr)
+    assert_route_equal(plan, r)
+    S = plan.num_slots
+    print(f"{name} rows at full size: T={T} d={d} E={E} S={S}", flush=True)
+    act = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    X = torch.randn(T, d, device=dev, generator=g).to(act)
+    YP = torch.randn(S, d, device=dev, generator=g).to(act)
+    DY = (torch.randn(T, d, device=dev, generator=g) * 0.02).to(act)
+    DXP = torch.randn(S, d, device=dev, generator=g).to(act)
+
+    def hostbits(t):
+        t = t.detach()
+        return t.view(torch.int16).cpu().numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+    x, yp, dy, dxp = hostbits(X), hostbits(YP), hostbits(DY), hostbits(DXP)
+    eq = lambda a, b: np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))  # noqa: E731
+    assert eq(hostbits(et.dispatch(X, plan)), orc.dispatch_fwd(x, r)), "dispatch"
+    assert eq(hostbits(et.combine(YP, plan)), orc.combine_fwd(yp, r, T)), "combine"
+    assert eq(hostbits(et.dispatch_backward(DXP, plan)), orc.dispatch_bwd(dxp, r, T)), "dispatch backward"
+    del X, DXP
+    dyp_g, dgate_g, dl_g = et.combine_backward(DY, YP, plan, need_dlogits=True)
+    dyp_o, dgate_o, dl_o = orc.combine_bwd(dy, yp, r, E, want_dlogits=True)
+    assert eq(hostbits(dyp_g), dyp_o), "dYp"
+    del dyp_g, dyp_o
+    f64 = (lambda a: orc.bf16_to_f32(a).astype(np.float64)) if act == torch.bfloat16 else (lambda a: a.astype(np.float64))
+    mass = np.empty(S)
+    for a in range(0, S, 32768):                  # sum_c |dY Yp| per slot, in blocks
+        b = min(S, a + 32768)
+        mass[a:b] = np.abs(f64(dy[r.sorted_token[a:b]]) * f64(yp[a:b])).sum(1)
+    dgate_h = host(dgate_g)
+    assert_dgate(dgate_h, dgate_o, mass, d, f" {name}")
+    assert_dlogits(host(dl_g), dgate_h, r, E)
