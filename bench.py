@@ -61,7 +61,7 @@ def algorithmic_bytes(T: int, E: int, S: int, d: int, b: int) -> dict:
 
 
 def read_traffic(workload: str):
-    """Measured HBM bytes of one et_combine_bwd call (its two kernels), from the
+    """Measured HBM bytes of one et_combine_bwd call (its kernels), from the
     committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated), if
     one exists for the workload."""
     path = os.path.join(ROOT, "profiles", f"pmc_combine_bwd_{workload}.txt")
@@ -723,11 +723,13 @@ def main() -> int:
         gbs = abytes[name] / (stage_ms[name] * 1e-3) / 1e9
         kernels[name] = {"ms": round(stage_ms[name], 4), "GB/s": round(gbs, 1),
                          "frac": round(gbs * 1e9 / HBM_PEAK, 4), "bytes": abytes[name]}
-    # The dominant stage, et_combine_bwd, is two launches on one stream
-    # (combine_bwd_vec, then combine_bwd_finish); its event time covers both.
+    # The dominant stage, et_combine_bwd, is three launches on one stream
+    # (combine_bwd_order, combine_bwd_vec, combine_bwd_finish; the order pass
+    # only where the slots are walked in token windows); its event time covers
+    # all of them.
     dom = "combine_bwd"
     ach = abytes[dom] / (stage_ms[dom] * 1e-3) / 1e9
-    roofline = {"kernel": "combine_bwd (combine_bwd_vec + combine_bwd_finish)", "bound": "hbm",
+    roofline = {"kernel": "combine_bwd (combine_bwd_order + combine_bwd_vec + combine_bwd_finish)", "bound": "hbm",
                 "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": read_traffic(args.workload),
                 "algorithmic_bytes": abytes[dom], "ms": round(stage_ms[dom], 4)}

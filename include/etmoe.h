@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 8
+#define ET_ABI_VERSION 9
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -112,7 +112,7 @@ int et_route(const float* logits, const float* thr, int64_t num_tokens, int64_t 
  * et_route (bit-identical results); the call runs on the current device, whose
  * scratch address it looks up once (on its first call there).  Sizes whose
  * et_route_workspace_bytes(T, E) exceeds the scratch are rejected with
- * ET_ERR_WORKSPACE_TOO_SMALL: every T fits for E <= 384 (the workspace depends
+ * ET_ERR_WORKSPACE_TOO_SMALL: every T fits for E <= 408 (the workspace depends
  * on E and only weakly on T).  All calls on one GPU share the scratch: calls
  * that overlap in time on one GPU (different streams or host threads) race.
  * No counterpart in the reference: an extra entry point of this library.
@@ -142,9 +142,11 @@ int et_combine_fwd(const void* yp, const float* slot_gate, const int32_t* token_
                    const int32_t* token_slot, int64_t num_tokens, int64_t d, int dtype,
                    int64_t slot_capacity, void* y, void* stream);
 
-/* Bytes of device workspace et_combine_bwd needs: slot_capacity * ceil(d * elem / 1024)
- * doubles when a row is a whole number of 16-byte chunks, else 0.  The
- * workspace must be 8-byte aligned. */
+/* Bytes of device workspace et_combine_bwd needs when a row is a whole number
+ * of 16-byte chunks (else 0): slot_capacity * ceil(d * elem / 1024) doubles of
+ * partial dot products, then, from the next 256-byte boundary, the slot walk
+ * order (slot_capacity int32).  num_tokens does not enter.  The workspace must
+ * be 8-byte aligned. */
 size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype);
 
 /*
@@ -155,8 +157,8 @@ size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity,
  *   dlogits[t, e] = dgate[s] * (g * (1 - g)) in binary32, g = slot_gate[s];
  *                   0 elsewhere
  * dlogits (f32 [T, E]) may be NULL.
- * workspace holds the per-piece partial dot products (et_combine_bwd_workspace_bytes);
- * it may be NULL when that size is 0.
+ * workspace holds the per-piece partial dot products and the slot walk order
+ * (et_combine_bwd_workspace_bytes); it may be NULL when that size is 0.
  * Implements the combine backward of the path (no reference counterpart).
  */
 int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,

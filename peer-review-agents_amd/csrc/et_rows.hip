@@ -361,22 +361,147 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
     __syncthreads();
 }
 
-// Vector path, pass 1: one wave per 1 KiB piece of a token's row.
-// For every slot s of the token the wave writes its piece of dYp[s] and the
-// piece's partial dot <dY[t], Yp[s]> to part[s * npieces + p].  The partial
-// is formed in binary64: every product of two binary32 (or bf16) values is
-// exact in binary64, each lane sums its chunk's products in two fma chains
-// (even and odd elements, then added), and one DPP wave reduction sums the
-// lanes, so the partial carries about a dozen binary64 roundings.  Yp is read
-// once and dYp written once, both non-temporal.  The slot walk is that of
-// combine_fwd_vec: the next slot's chunk is loaded after the current slot's
-// store, so one load and one store are in flight per wave.  (Batching four
-// slots' loads ahead of their stores, with one reduction for the four, was
-// 1-9% slower across routing shapes, with or without the arithmetic: the
-// access order, not the binary64 work, sets the time.)  The wave of piece 0
-// also zero-fills the token's dlogits row; pass 2 then writes the routed
-// entries.
-constexpr int kBwdWaves = 2;
+// Vector path, pass 1.  For every routed slot s and every 1 KiB piece p of
+// the row, one wave writes that piece of dYp[s] = gate[s] * dY[token(s)] and
+// the piece's partial dot <dY[t], Yp[s]> to part[s * npieces + p].  The
+// partial is formed in binary64: every product of two binary32 (or bf16)
+// values is exact in binary64, each lane sums its chunk's products in two fma
+// chains (even and odd elements, then added), and one DPP wave reduction sums
+// the lanes, so the partial carries about a dozen binary64 roundings.  Yp is
+// read once and dYp written once, both non-temporal.
+//
+// Walk order.  Walking tokens (each token's ~k slots at once) has the waves in
+// flight touch a slot run in every expert block, each run visited again and
+// again over time, and walking slots in slot order re-reads each dY row k
+// times from HBM.  Instead the tokens are cut into windows of TW consecutive
+// tokens (TW dY rows, 3 MiB, re-read from the cache); inside a window each
+// expert's slots are one contiguous run (slots are ordered by token within an
+// expert), and the runs are walked one after another, so consecutive waves
+// take consecutive slots of one run.  At d = 4096 bf16, E = 128, k = 8 this is
+// 8-9% faster than the token walk (Zipf-skewed and uniform expert loads); with
+// about one slot per token, or a dY that the caches hold, the plain slot order
+// (s = J, no order pass) is faster still and is used instead.  The
+// window-ordered index of slot s is
+//     J(s) = base[w] + pre[w][e] + (s - off[w][e]),  w = token(s) / TW, e = expert(s)
+// with off[w][e] = the first slot of expert e whose token is >= w * TW,
+// pre[w][e] = the window's slots in experts < e and base[w] =
+// token_offsets[w * TW] (the slots of the tokens before the window).  One
+// small kernel builds order[J(s)] = s; the main kernel walks J with one wave
+// per (J, pair of pieces).  Each XCD (block b runs on XCD b % 8) takes a
+// contiguous eighth of the J range, so one XCD's L2 holds the dY rows of the
+// window it walks: windows are sized at 3 MiB of dY for the 4 MB L2 of an
+// XCD (4 MiB and more thrash it; measured 3-15% slower).
+//
+// When the routed slots exceed an undersized capacity (expert_offsets[E] >
+// cap) the order pass writes nothing and the main kernel walks the token
+// lists instead: J in [0, cap), s = token_slot[J], skipping s >= cap -- the
+// (slot, piece) pairs a token-major walk of the capacity-clamped lists visits.
+// Either way each (slot, piece) partial is formed the same way, so the
+// results do not depend on the order.
+constexpr int kBwdWaves = 1;
+constexpr int kWinPieces = 2;                    // 1 KiB row pieces per wave
+constexpr int64_t kWinBytes = int64_t(3) << 20;  // dY bytes of one token window (target)
+constexpr int kXcds = 8;
+
+static int64_t win_tokens(int64_t rb)
+{
+    return std::min<int64_t>(8192, std::max<int64_t>(64, kWinBytes / std::max<int64_t>(rb, 1)));
+}
+
+// Slot order (no windows) where windows do not pay for their order pass:
+// about one slot per token (capacity <= 1.25 T, so dY rows are not re-read),
+// or a dY small enough to stay in the caches.
+constexpr int64_t kSlotOrderBytes = int64_t(16) << 20;
+
+static bool bwd_slot_order(int64_t T, int64_t cap, int64_t rb)
+{
+    return cap * 4 <= T * 5 || T * rb <= kSlotOrderBytes;
+}
+
+// order[J(s)] = s for the slots of one token window per block.  The
+// window's token-list entries are [j0, j1) = [token_offsets[w TW],
+// token_offsets[(w + 1) TW]), which is also its range of J.  The block counts
+// the window's slots per expert and finds each expert's first slot (LDS
+// atomics: add and min, so the result does not depend on their order), scans
+// the counts, then places every slot.  Each thread loads kOrderBatch entries
+// before using any, so a window of up to kOrderThreads * kOrderBatch entries
+// pays one memory latency per pass.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBatch = 8;
+
+// Slots of token-list entries jb + k * kOrderThreads + threadIdx.x (k <
+// kOrderBatch) below j1, with their experts; -1 where out of range.
+__device__ __forceinline__ void order_batch(const int32_t* __restrict__ tok_slot, int64_t jb, int64_t j1, int64_t S,
+                                            const int32_t* eo, int E, int (&sv)[kOrderBatch], int (&ev)[kOrderBatch])
+{
+#pragma unroll
+    for (int k = 0; k < kOrderBatch; ++k) {
+        const int64_t j = jb + (int64_t)k * kOrderThreads + threadIdx.x;
+        sv[k] = j < j1 ? tok_slot[j] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kOrderBatch; ++k) {
+        if (sv[k] < 0 || (int64_t)sv[k] >= S) sv[k] = -1;
+        ev[k] = sv[k] >= 0 ? expert_of_slot(eo, E, sv[k]) : 0;
+    }
+}
+
+__global__ __launch_bounds__(kOrderThreads) void combine_bwd_order(
+    const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff,
+    int E, int T, int TW, int64_t cap, int32_t* __restrict__ order)
+{
+    extern __shared__ int32_t sh[];                 // eo [E + 1], cnt [E], first [E]
+    int32_t* eo = sh;
+    int32_t* cnt = sh + E + 1;
+    int32_t* first = cnt + E;
+    const int64_t t0 = (int64_t)blockIdx.x * TW;
+    const int64_t t1 = min(t0 + TW, (int64_t)T);
+    for (int e = threadIdx.x; e <= E; e += kOrderThreads) {
+        eo[e] = eoff[e];
+        if (e < E) {
+            cnt[e] = 0;
+            first[e] = INT32_MAX;
+        }
+    }
+    __syncthreads();
+    const int64_t S = eo[E];
+    if (S > cap) return;                            // undersized: pass 1 walks the token lists
+    const int64_t j0 = min(max((int64_t)tok_off[t0], (int64_t)0), S);
+    const int64_t j1 = max(min((int64_t)tok_off[t1], S), j0);
+    constexpr int64_t kStep = (int64_t)kOrderThreads * kOrderBatch;
+    for (int64_t jb = j0; jb < j1; jb += kStep) {
+        int sv[kOrderBatch], ev[kOrderBatch];
+        order_batch(tok_slot, jb, j1, S, eo, E, sv, ev);
+#pragma unroll
+        for (int k = 0; k < kOrderBatch; ++k)
+            if (sv[k] >= 0) {
+                atomicAdd(&cnt[ev[k]], 1);
+                atomicMin(&first[ev[k]], sv[k]);
+            }
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave) {                      // exclusive scan of cnt, in place
+        int run = 0;
+        for (int e0 = 0; e0 < E; e0 += kWave) {
+            const int e = e0 + (int)threadIdx.x;
+            const int c = e < E ? cnt[e] : 0;
+            const int incl = wave_incl_scan(c);
+            if (e < E) cnt[e] = run + incl - c;
+            run += __builtin_amdgcn_readlane(incl, kWave - 1);
+        }
+    }
+    __syncthreads();
+    for (int64_t jb = j0; jb < j1; jb += kStep) {
+        int sv[kOrderBatch], ev[kOrderBatch];
+        order_batch(tok_slot, jb, j1, S, eo, E, sv, ev);
+#pragma unroll
+        for (int k = 0; k < kOrderBatch; ++k)
+            if (sv[k] >= 0) {
+                const int64_t J = j0 + cnt[ev[k]] + ((int64_t)sv[k] - first[ev[k]]);
+                if (J >= j0 && J < j1) order[J] = sv[k];
+            }
+    }
+}
 
 template <int N>
 __device__ __forceinline__ double dot_f64(const double (&dd)[N], const float (&f)[N])
@@ -391,61 +516,83 @@ __device__ __forceinline__ double dot_f64(const double (&dd)[N], const float (&f
     return a0 + a1;
 }
 
+// The main pass: one wave per (J, pair of pieces); both pieces' loads are
+// issued before either is used.  The first waves in dispatch order also
+// zero-fill dlogits (1 KiB each), which pass 2 then writes at the routed
+// entries.
 template <int DT>
 __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
-    const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate, int t_base,
-    int t_end, int64_t nch, uint32_t npieces, const int32_t* __restrict__ tok_off,
-    const int32_t* __restrict__ tok_slot, int64_t cap, int E, char* __restrict__ dyp,
-    double* __restrict__ part, float* __restrict__ dlogits)
+    const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate,
+    const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff, int E, int T, int64_t nch,
+    uint32_t npieces, int64_t cap, char* __restrict__ dyp, double* __restrict__ part, float* __restrict__ dlogits)
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
-    PieceSpan sp;
-    if (!piece_span<kBwdWaves>(t_base, t_end, npieces, kWave, tok_off, cap, sp)) return;
+    const int64_t S = eoff[E];
+    const bool fits = S <= cap;
+    const int32_t* __restrict__ walk = fits ? order : tok_slot;     // null: slot order (s = J)
+    const int64_t nj = fits ? S : cap;
     const int lane = lane_id();
-    const int64_t idx = sp.cb + lane;
-    const bool on = idx < nch;
     const int64_t rb = nch * 16;
-    const uint32_t p = (uint32_t)(sp.cb / kWave);
-    if (dlogits && p == 0)
-        for (int e = lane; e < E; e += kWave) dlogits[(int64_t)sp.t * E + e] = 0.0f;
-    float df[N];
-    double dd[N];
-    {
-        v4u w = {0u, 0u, 0u, 0u};
-        if (on) w = ld16(dy + (int64_t)sp.t * rb + idx * 16);
-        P::unpack(w, df);
+    const uint32_t nq = (npieces + kWinPieces - 1) / kWinPieces;
+    const int64_t items = nj * nq;
+    // XCD-contiguous order: the items' blocks are split into kXcds
+    // contiguous ranges of `per` blocks; the blocks b with b % kXcds == x walk
+    // range x (the grid is a multiple of kXcds blocks)
+    const int64_t per = ((items + kBwdWaves - 1) / kBwdWaves + kXcds - 1) / kXcds;
+    const int64_t rows = gridDim.x / kXcds;
+    const int64_t x0 = (int64_t)(blockIdx.x % kXcds) * per;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    if (dlogits) {
+        const int64_t n = (int64_t)T * E;
+        const int64_t stride = (int64_t)gridDim.x * kBwdWaves * 4 * kWave;
+        for (int64_t f = ((int64_t)blockIdx.x * kBwdWaves + wv) * 4 * kWave; f < n; f += stride)
 #pragma unroll
-        for (int i = 0; i < N; ++i) dd[i] = (double)df[i];
+            for (int k = 0; k < 4; ++k)
+                if (f + k * kWave + lane < n) dlogits[f + k * kWave + lane] = 0.0f;
     }
-    for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
-        const int my = load_slot_block(tok_slot, jb, sp.j1);
-        const int n = min(kWave, sp.j1 - jb);
-        // slot walk as in combine_fwd_vec
-        int u = 0;
-        int s = -1;
-        v4u w = {0u, 0u, 0u, 0u};
-        for (; u < n; ++u) {
-            s = __builtin_amdgcn_readlane(my, u);
-            if (s >= 0 && (int64_t)s < cap) break;
-        }
-        if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
-        while (u < n) {
-            const int cur = s;
-            const v4u wc = w;
-            for (++u; u < n; ++u) {
-                s = __builtin_amdgcn_readlane(my, u);
-                if (s >= 0 && (int64_t)s < cap) break;
-            }
-            const float g = gate[cur];
-            float f[N], o[N];
-            P::unpack(wc, f);
+    for (int64_t row = blockIdx.x / kXcds; row < per; row += rows) {
+        const int64_t it = (x0 + row) * kBwdWaves + wv;
+        if (it >= items) break;
+        const int64_t J = it / nq;
+        const uint32_t q = (uint32_t)(it - J * nq);
+        const int s = walk ? walk[J] : (int)J;
+        if (s < 0 || (int64_t)s >= cap || (int64_t)s >= S) continue;
+        const int t = sorted_token[s];
+        if (t < 0 || t >= T) continue;
+        const float g = gate[s];
+        int64_t idx[kWinPieces];
+        bool on[kWinPieces];
+        v4u wy[kWinPieces], wd[kWinPieces];
 #pragma unroll
-            for (int i = 0; i < N; ++i) o[i] = g * df[i];
-            if (on) st16_nt(dyp + (int64_t)cur * rb + idx * 16, P::pack(o));
-            const double dot = wave_sum_dpp_f64(dot_f64<N>(dd, f));
-            if (lane == 0) part[(int64_t)cur * npieces + p] = dot;
-            if (u < n && on) w = ld16_nt(yp + (int64_t)s * rb + idx * 16);
+        for (int i = 0; i < kWinPieces; ++i) {
+            idx[i] = (int64_t)(q * kWinPieces + i) * kWave + lane;
+            on[i] = idx[i] < nch;
+            wy[i] = v4u{0u, 0u, 0u, 0u};
+            wd[i] = v4u{0u, 0u, 0u, 0u};
+            if (on[i]) {
+                wy[i] = ld16_nt(yp + (int64_t)s * rb + idx[i] * 16);
+                wd[i] = ld16(dy + (int64_t)t * rb + idx[i] * 16);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kWinPieces; ++i) {
+            float f[N], df[N], o[N];
+            double dd[N];
+            P::unpack(wy[i], f);
+            P::unpack(wd[i], df);
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                dd[k] = (double)df[k];
+                o[k] = g * df[k];
+            }
+            if (on[i]) st16_nt(dyp + (int64_t)s * rb + idx[i] * 16, P::pack(o));
+            const uint32_t p = q * kWinPieces + i;
+            if (p < npieces) {
+                const double dot = wave_sum_dpp_f64(dot_f64<N>(dd, f));
+                if (lane == 0) part[(int64_t)s * npieces + p] = dot;
+            }
         }
     }
 }
@@ -733,14 +880,17 @@ extern "C" int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offs
 
 static bool bwd_vector_path(int64_t d, int dtype) { return d > 0 && (d * elem_bytes(dtype)) % 16 == 0; }
 
+// Workspace of the vector path: the binary64 partial dots [cap * npieces],
+// then the slot order [cap] int32 at the next 256-byte boundary.
+static size_t bwd_order_offset(int64_t cap, int64_t np) { return ((size_t)(cap * np) * sizeof(double) + 255) & ~(size_t)255; }
+
 extern "C" size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype)
 {
     (void)num_tokens;
     if (slot_capacity < 0 || d < 0 || (dtype != ET_DTYPE_F32 && dtype != ET_DTYPE_BF16)) return 0;
     if (!bwd_vector_path(d, dtype)) return 0;
-    const int64_t nch = d * elem_bytes(dtype) / 16;
-    const int64_t np = (nch + kWave - 1) / kWave;
-    return (size_t)(slot_capacity * np) * sizeof(double);
+    const int64_t np = (d * elem_bytes(dtype) / 16 + kWave - 1) / kWave;
+    return bwd_order_offset(slot_capacity, np) + (size_t)slot_capacity * 4;
 }
 
 extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
@@ -770,17 +920,34 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
                                                         " bytes, got " + std::to_string(workspace_bytes));
         if ((reinterpret_cast<uintptr_t>(workspace) & 7) != 0)
             return fail(ET_ERR_INVALID_ARGUMENT, "et_combine_bwd: workspace must be 8-byte aligned");
-        double* part = static_cast<double*>(workspace);
         const int64_t nch = rb / 16;
         const int64_t np = (nch + kWave - 1) / kWave;
-        for_each_piece_launch(T, np, kBwdWaves, [&](dim3 grid, int t0, int t1) {
-            ET_SWITCH_DT(dtype, combine_bwd_vec<DT><<<grid, dim3(kBwdWaves * kWave), 0, s>>>(
-                                    dyc, ypc, slot_gate, t0, t1, nch, (uint32_t)np, token_offsets, token_slot, cap,
-                                    (int)E, dypc, part, dlogits));
-        });
-        if (int rc = check_launch("combine_bwd_vec")) return rc;
-        if (cap == 0) return ET_OK;
+        const int64_t TW = win_tokens(rb);
+        const int64_t nw = (T + TW - 1) / TW;
+        char* wsb = static_cast<char*>(workspace);
+        double* part = reinterpret_cast<double*>(wsb);
+        int32_t* order = nullptr;
+        if (cap > 0 && !bwd_slot_order(T, cap, rb)) {
+            order = reinterpret_cast<int32_t*>(wsb + bwd_order_offset(cap, np));
+            combine_bwd_order<<<dim3((unsigned)nw), dim3(kOrderThreads), (size_t)(3 * E + 1) * 4, s>>>(
+                token_offsets, token_slot, expert_offsets, (int)E, (int)T, (int)TW, cap, order);
+            if (int rc = check_launch("combine_bwd_order")) return rc;
+        }
         const size_t lds = (size_t)(E + 1) * 4;
+        {
+            // one wave per (slot, pair of pieces) for every slot the capacity
+            // holds (the waves past the routed count exit at once), in a grid
+            // of whole XCD rounds; with capacity 0 it only zero-fills dlogits
+            const int64_t nq = (np + kWinPieces - 1) / kWinPieces;
+            const int64_t blocks =
+                std::max<int64_t>(1, std::min<int64_t>((cap * nq + kBwdWaves - 1) / kBwdWaves, int64_t(1) << 29));
+            const int64_t grid = (blocks + kXcds - 1) / kXcds * kXcds;
+            ET_SWITCH_DT(dtype, combine_bwd_vec<DT><<<dim3((unsigned)grid), dim3(kBwdWaves * kWave), 0, s>>>(
+                                    dyc, ypc, slot_gate, sorted_token, order, token_slot, expert_offsets, (int)E,
+                                    (int)T, nch, (uint32_t)np, cap, dypc, part, dlogits));
+            if (int rc = check_launch("combine_bwd_vec")) return rc;
+        }
+        if (cap == 0) return ET_OK;
         combine_bwd_finish<<<dim3((unsigned)((cap + kFinishThreads - 1) / kFinishThreads)), dim3(kFinishThreads),
                              lds, s>>>(part, (uint32_t)np, slot_gate, sorted_token, token_offsets, token_slot,
                                        expert_offsets, (int)E, cap, dgate, dlogits);

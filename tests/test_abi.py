@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 8" in hdr
-    assert et.lib().et_abi_version() == 8
+    assert "#define ET_ABI_VERSION 9" in hdr
+    assert et.lib().et_abi_version() == 9
 
 
 def test_workspace_sizes(et):
@@ -121,9 +121,12 @@ def test_error_string_is_per_call(et):
 
 def test_combine_bwd_workspace(et):
     lib = et.lib()
-    # one binary64 partial per slot and 1 KiB piece of the row (C3: d = 4096 bf16 -> 8 pieces)
-    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == 528736 * 8 * 8
-    assert lib.et_combine_bwd_workspace_bytes(4096, 8192, 512, 0) == 8192 * 2 * 8
+    # one binary64 partial per slot and 1 KiB piece of the row (C3: d = 4096 bf16 -> 8
+    # pieces), then the slot walk order (one int32 per slot) from a 256-byte boundary
+    r = lambda x: (x + 255) // 256 * 256
+    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == r(528736 * 8 * 8) + 528736 * 4
+    assert lib.et_combine_bwd_workspace_bytes(4096, 8191, 512, 0) == r(8191 * 2 * 8) + 8191 * 4
+    assert lib.et_combine_bwd_workspace_bytes(1, 8191, 512, 0) == r(8191 * 2 * 8) + 8191 * 4
     assert lib.et_combine_bwd_workspace_bytes(10, 100, 7, 1) == 0        # element path: none
     assert lib.et_combine_bwd_workspace_bytes(10, 100, 8, 5) == 0        # bad dtype
     p = ctypes.c_void_p(0x1000)                   # 16-byte aligned: the vector path is chosen
@@ -131,8 +134,9 @@ def test_combine_bwd_workspace(et):
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL and "workspace" in _err(et)
     rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, p, 63, None)
     assert rc == ET_ERR_WORKSPACE_TOO_SMALL
+    need = lib.et_combine_bwd_workspace_bytes(8, 8, 64, 1)
     odd = ctypes.c_void_p(0x1004)                 # the binary64 partials need 8-byte alignment
-    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, odd, 64, None)
+    rc = lib.et_combine_bwd(p, p, p, p, p, p, p, 8, 4, 64, 1, 8, p, p, p, odd, need, None)
     assert rc == ET_ERR_INVALID_ARGUMENT and "aligned" in _err(et)
 
 

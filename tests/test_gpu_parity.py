@@ -273,6 +273,32 @@ def test_rows_shapes(et, orc, dev, d, dtype):
     check_rows(et, orc, dev, lg, thr, d, dtype, seed=d)
 
 
+@pytest.mark.parametrize("E,mode", [(24, "quantile"), (24, "fallback"), (4, "all")])
+def test_rows_token_windows(et, orc, dev, E, mode):
+    """Combine backward walks the slots in token windows (3 MiB of dY rows:
+    192 tokens at d = 8192 bf16) when dY exceeds 16 MiB and there is more than
+    about one slot per token: T = 1100 gives five full windows and a ragged
+    one (quantile and all-selected routing); fallback routing (one slot per
+    token) takes the plain slot order.  Also with spare slot capacity (S <
+    capacity): the same dYp, dgate and dlogits bits."""
+    T, d = 1100, 8192
+    lg, thr = synthetic_router(T, E, mode, seed=E)
+    check_rows(et, orc, dev, lg, thr, d, "bf16", seed=5)
+    r = orc.route(lg, thr)
+    S = r.num_slots
+    x, yp, dy, _ = make_rows(orc, r, T, d, "bf16", 5)
+    exact = et.route(dev_f32(lg, dev), dev_f32(thr, dev))
+    spare = et.route(dev_f32(lg, dev), dev_f32(thr, dev), slot_capacity=S + 37)
+    DY = to_dev(dy, dev)
+    YP = to_dev(yp, dev)
+    YP2 = torch.cat([YP, torch.zeros(37, d, dtype=YP.dtype, device=dev)])
+    dyp_a, dgate_a, dl_a = et.combine_backward(DY, YP, exact, need_dlogits=True)
+    dyp_b, dgate_b, dl_b = et.combine_backward(DY, YP2, spare, need_dlogits=True)
+    assert torch.equal(dyp_a.view(torch.int16), dyp_b[:S].view(torch.int16))
+    assert torch.equal(dgate_a.view(torch.int32), dgate_b[:S].view(torch.int32))
+    assert torch.equal(dl_a.view(torch.int32), dl_b.view(torch.int32))
+
+
 @pytest.mark.parametrize("mode", ["fallback", "all", "special"])
 def test_rows_routing_modes(et, orc, dev, mode):
     lg, thr = synthetic_router(200, 24, mode, seed=9)
