@@ -8,12 +8,16 @@ logits GEMM (exact on integer inputs) and the fused producer + routing
 
 Each case draws T, E, d, the activation dtype and a routing mode (per-expert
 quantile thresholds, all-fallback, all-selected, NaN/inf/tie specials); sizes
-are kept small enough for the oracle to finish in well under a second."""
+are kept small enough for the oracle to finish in well under a second.  Those
+shapes all walk combine backward's slots in plain slot order (dY <= 16 MiB), so
+a second set draws shapes above that size with more than 1.25 slots per token,
+which take the token-window walk."""
 import numpy as np
 import pytest
 import torch
 
-from test_gpu_parity import check_rows, dev_f32, host, make_rows, synthetic_router, to_dev
+from test_gpu_parity import (assert_dgate, assert_dlogits, bits, check_rows, dev_f32, host, make_rows,
+                             synthetic_router, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -73,3 +77,56 @@ def test_random_shape_whole_path(et, orc, dev, seed):
         for f in ("counts", "expert_offsets", "token_offsets", "sorted_token", "token_slot"):
             assert torch.equal(getattr(a, f), getattr(b, f)), f
         assert torch.equal(a.slot_gate.view(torch.int32), b.slot_gate.view(torch.int32))
+
+
+def draw_windowed(seed):
+    """A shape whose combine backward walks token windows: dY above 16 MiB
+    and more than 1.25 slots per token (so the quantile or all-selected
+    routing), with S * d kept near 40M elements or below."""
+    rng = np.random.default_rng([2025, seed])
+    dtype = str(rng.choice(["f32", "bf16"]))
+    b = 4 if dtype == "f32" else 2
+    mode = str(rng.choice(["quantile", "quantile", "all"]))
+    d = int(rng.choice([1032, 2048, 3000, 4096, 8192, 12288]))
+    t_min = (16 << 20) // (d * b) + 1
+    # quantile routing selects about E / 4 experts per token: keep S * d <= 60M
+    e_max = 60e6 / (0.25 * d * t_min)
+    E = (int(rng.choice([e for e in [6, 8, 13, 31, 33, 64, 65, 100, 129] if e <= e_max] or [6]))
+         if mode == "quantile" else int(rng.choice([2, 3, 4])))
+    k = E * 0.25 if mode == "quantile" else E
+    t_max = max(t_min, int(40e6 // max(1.0, k * d)))
+    T = int(rng.integers(t_min, max(t_min + 1, min(t_max, 3 * t_min))))
+    return T, d, E, dtype, mode
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shape_windowed_combine_backward(et, orc, dev, seed):
+    """Combine backward on random shapes that take the token-window walk
+    (windows of 3 MiB of dY rows, so 2 to ~30 windows, the last one ragged):
+    dYp bit-exact, dgate within the binary32 bar, dlogits bit-exact from
+    dgate, against the oracle; also with spare slot capacity."""
+    T, d, E, dtype, mode = draw_windowed(seed)
+    print(f"windowed case {seed}: T={T} d={d} E={E} {dtype} {mode}", flush=True)
+    lg, thr = synthetic_router(T, E, mode, seed)
+    r = orc.route(lg, thr)
+    S = r.num_slots
+    assert S * 4 > T * 5 and T * d * (4 if dtype == "f32" else 2) > 16 << 20    # the windowed rule holds
+    plan = et.route(dev_f32(lg, dev), dev_f32(thr, dev))
+    _, yp, dy, _ = make_rows(orc, r, T, d, dtype, seed)
+    DY, YP = to_dev(dy, dev), to_dev(yp, dev)
+    dyp_g, dgate_g, dl_g = et.combine_backward(DY, YP, plan, need_dlogits=True)
+    dyp_o, dgate_o, _ = orc.combine_bwd(dy, yp, r, E, want_dlogits=True)
+    np.testing.assert_array_equal(bits(host(dyp_g)), bits(dyp_o))
+    cvt = orc.bf16_to_f32 if dtype == "bf16" else (lambda a: a)
+    mass = np.einsum("sd,sd->s", np.abs(cvt(dy)[r.sorted_token].astype(np.float64)),
+                     np.abs(cvt(yp).astype(np.float64)))
+    dgate_h = host(dgate_g)
+    assert_dgate(dgate_h, dgate_o, mass, d)
+    assert_dlogits(host(dl_g), dgate_h, r, E)
+    spare = et.route(dev_f32(lg, dev), dev_f32(thr, dev), slot_capacity=S + 129)
+    YP2 = torch.cat([YP, torch.zeros(129, d, dtype=YP.dtype, device=dev)])
+    dyp_b, dgate_b, dl_b = et.combine_backward(DY, YP2, spare, need_dlogits=True)
+    iv = (lambda t: t.view(torch.int16)) if dtype == "bf16" else (lambda t: t.view(torch.int32))
+    assert torch.equal(iv(dyp_b[:S]), iv(dyp_g))
+    assert torch.equal(dgate_b[:S].view(torch.int32), dgate_g.view(torch.int32))
+    assert torch.equal(dl_b.view(torch.int32), dl_g.view(torch.int32))
