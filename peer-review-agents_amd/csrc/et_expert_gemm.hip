@@ -11,8 +11,14 @@
 // nn.Linear layout (row n of expert e is output feature n).
 //
 // Tiling.  A block of 4 waves owns 256 slots x 256 output features of one
-// expert; wave (wm, wn) owns 128 x 128 of it, 4 x 4 tiles of
-// v_mfma_f32_32x32x16_bf16.  K advances in chunks of 64 through two LDS stages
+// expert; wave (wm, wn) owns 128 x 128 of it: 8 x 8 tiles of
+// v_mfma_f32_16x16x32_bf16 (bf16), or 4 x 4 tiles of
+// v_mfma_scale_f32_32x32x64_f8f6f4 (fp8).  The 16 x 16 bf16 form moves half
+// the accumulator bytes per FLOP of v_mfma_f32_32x32x16_bf16 and draws less
+// power: with the same fragment reads, a sustained MFMA loop on every CU ran
+// 16% faster with it, and this kernel runs at a 13% higher clock (its time
+// changed by -3.4% to +0.4%: the operand stream, not the clock, bounds it).
+// K advances in chunks of 64 through two LDS stages
 // filled by gfx950's direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds),
 // with no staging registers.  A wave holds a whole chunk's MFMA fragments in
 // registers, so a stage is free again as soon as every wave has read it, and
@@ -22,22 +28,22 @@
 // runs ~45% faster this way than with 32 rows x 32 bytes per instruction, the
 // MFMA fragment's own shape).  So a stage holds each operand row-major, 128
 // bytes (64 k) per row, and the 16-byte segment s of row R sits at slot
-// s ^ key(R), key(R) = (R & 7) ^ ((R >> 3) & 1): the fragment reads (lane l:
-// row l % 32, segment 2 * kstep + l / 32) then hit 16 distinct slots of every
-// 256-byte bank window, with no bank conflicts.  The output goes straight
-// from the accumulators to memory (16 bytes per lane after a lane-pair swap),
-// leaving the stages to the next tile.
+// s ^ key(R), key(R) = (R & 7) ^ ((R >> 3) & 1): the fragment reads (bf16:
+// lane l reads row l % 16, segment 4 * kstep + l / 16) then hit 16 distinct
+// slots of every 256-byte bank window, with no bank conflicts.  The output
+// goes straight from the accumulators to memory (16 bytes per lane after a
+// lane-row swap), leaving the stages to the next tile.
 //
-// MFMA 32x32x16 bf16 operand layout (checked on the device by the router
-// kernels): lane l holds A row l % 32 and B column l % 32 at k = 8 (l / 32) + i;
-// C column l % 32, acc[j] at row 8 (j / 4) + 4 (l / 32) + j % 4.  The product
-// is issued as mfma(W fragment, X fragment) so that C's columns are slots and
-// its rows output features: each lane then holds 4 consecutive features of
-// one slot per j / 4, stored as one 8-byte write.
+// MFMA 16x16x32 bf16 operand layout (checked on the device): lane l holds A
+// row l % 16 and B column l % 16 at k = 8 (l / 16) + i; C column l % 16,
+// acc[r] at row 4 (l / 16) + r.  The product is issued as mfma(W fragment, X
+// fragment) so that C's columns are slots and its rows output features: each
+// lane then holds 4 consecutive features of one slot.
 //
-// Order of the sum.  Every output sums its k-steps of 16 in ascending k, each
-// k-step inside one MFMA; so results depend on K only, not on the tile, the
-// expert or the mode, and the gather and slot-major modes give identical bits.
+// Order of the sum.  Every output sums its k-steps (32 k for bf16, 64 for
+// fp8) in ascending k, each k-step inside one MFMA; so results depend on K
+// only, not on the tile, the expert or the mode, and the gather and
+// slot-major modes give identical bits.
 //
 // Schedule.  The grid is persistent (a multiple of 8 blocks, at most one per
 // CU).  Each block computes the per-expert tile prefix once, then walks its
@@ -60,6 +66,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
@@ -156,6 +163,24 @@ __device__ __forceinline__ void store_row_segment(u32x2_t (&P)[4], __amdgpu_buff
     }
 }
 
+// Output of two 16 x 16 accumulator tiles side by side (output columns col0
+// ... col0 + 31 of one slot): lane l (16-lane row rho = l / 16) holds columns
+// 4 rho + 0..3 of the first tile in v[0..3] and of the second in v[4..7].
+// v_permlane16_swap exchanges the odd 16-lane rows of its first operand with
+// the even rows of its second (lane layout checked on the device), after
+// which lane l holds columns 16 (rho & 1) + 8 (rho >> 1) + 0..7, stored as one
+// 16-byte write (range-checked offset; ncols is a multiple of 8).
+__device__ __forceinline__ void store_pair16(const float (&v)[8], __amdgpu_buffer_rsrc_t res, bool row_ok,
+                                             uint32_t row_base, int col0, int ncols, int rho)
+{
+    const auto lo = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[4], v[5]), false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v[2], v[3]), pack_bf16x2(v[6], v[7]), false, false);
+    const u32x4_t out = {lo[0], hi[0], lo[1], hi[1]};
+    const int col = col0 + 16 * (rho & 1) + 8 * (rho >> 1);
+    const uint32_t off = (row_ok && col < ncols) ? (row_base + (uint32_t)col) * 2u : kOOR;
+    __builtin_amdgcn_raw_buffer_store_b128(out, res, off, 0, 0);
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight,
 // then meet the other waves.  The direct-to-LDS loads count in vmcnt and are
 // in LDS once it has dropped, so after the barrier every wave's loads of the
@@ -182,7 +207,9 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
 {
     constexpr int ES = FP8 ? 1 : 2;           // bytes per element
     constexpr int KC = 128 / ES;              // k per chunk (one 128-byte row)
-    constexpr int NKS = FP8 ? 2 : 4;          // k-steps per chunk
+    constexpr int NKS = 2;                    // k-steps per chunk (32 k bf16, 64 k fp8)
+    constexpr int TS = FP8 ? 32 : 16;         // MFMA tile side
+    constexpr int TM = 128 / TS;              // MFMA tiles per wave and dimension
     // the two operand stages
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
@@ -226,6 +253,8 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int xcd = (int)(blockIdx.x & 7);
     const int r32 = lane & 31;
     const int kh = lane >> 5;
+    const int r16 = lane & 15;
+    const int rho = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
     const int nk = (K + KC - 1) / KC;
 
@@ -367,12 +396,13 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int R = 64 * wave + 8 * i + (lane >> 3);
         const uint32_t seg = (uint32_t)segk[i & 1] * ES;
         if constexpr (EPI == EPI_SWIGLU) {
-            // tile row R -> wave column half R / 128, MFMA tile (R / 32) % 4
-            // (0, 1: gate; 2, 3: up), so a wave's gate and up accumulators
-            // of one hidden unit sit in the same lane and register
-            const int tt = (R >> 5) & 3;
-            const int hid = t.n0 + (R >> 7) * 64 + (tt & 1) * 32 + (R & 31);
-            return hid < F ? (uint32_t)(tt >= 2 ? F + hid : hid) * ((uint32_t)K * ES) + seg : kOOR;
+            // tile row R -> wave column half R / 128, MFMA tile tt of the
+            // half (bf16: 16 rows, 0..3 gate, 4..7 up; fp8: 32 rows, 0, 1
+            // gate, 2, 3 up), so a wave's gate and up accumulators of one
+            // hidden unit sit in the same lane and register
+            const int tt = (R & 127) / TS;
+            const int hid = t.n0 + (R >> 7) * 64 + (tt % (TM / 2)) * TS + (R & (TS - 1));
+            return hid < F ? (uint32_t)(tt >= TM / 2 ? F + hid : hid) * ((uint32_t)K * ES) + seg : kOOR;
         } else {
             const int n = t.n0 + R;
             return n < N ? (uint32_t)n * ((uint32_t)K * ES) + seg : kOOR;
@@ -394,52 +424,54 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         else dma_b128(t.ares, a_off(t, o, i, tb) | kmask, soff, sb);
     };
 
-    f32x16_t acc[4][4];
+    using Acc = std::conditional_t<FP8, f32x16_t, f32x4_t>;
+    Acc acc[TM][TM];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+        for (int j = 0; j < TM; ++j) acc[i][j] = Acc{};
 
-    // Fragment of tile t (32 rows), k-step ks: lane l reads row R = 32 t +
-    // l % 32, segment 2 ks + l / 32, at 1024 (R / 8) + 128 (R % 8) +
-    // 16 ((2 ks + l / 32) ^ key(R)); key(R) = (l % 8) ^ ((l / 8) & 1).
+    // Fragment of tile t (TS rows), k-step ks: lane l reads row R = TS t +
+    // l % TS, at 1024 (R / 8) + 128 (R % 8) + 16 (segment ^ key(R)),
+    // key(R) = (l % 8) ^ ((l / 8) & 1) (TS is a multiple of 16); the segment
+    // is 4 ks + l / 16 (bf16) or 4 ks + 2 (l / 32) + piece (fp8).  A 16-lane
+    // group reads 16 rows or one row group pair at 16 distinct slots of a
+    // 256-byte window: no bank conflicts.
     const int fkey = (lane & 7) ^ ((lane >> 3) & 1);
-    const int flane = ((lane & 31) >> 3) * 1024 + (lane & 7) * 128;
+    const int flane = ((lane & (TS - 1)) >> 3) * 1024 + (lane & 7) * 128;
     const unsigned char* const abase = smem + wm * 16384 + flane;
     const unsigned char* const bbase = smem + kHalf + wn * 16384 + flane;
     // A whole chunk's fragments, [k-step][A, W][tile]: 16 bytes per lane
     // (bf16) or 32 (fp8, filled by two reads).
     using Frag = std::conditional_t<FP8, u32x8_t, u32x4_t>;
-    Frag f[NKS][2][4];
+    Frag f[NKS][2][TM];
     // Read r of k-step ks of the chunk in stage st, r < RPK: fragment q = r
-    // (bf16) or r / 2 (fp8, piece r % 2); q < 4: A tile q, else W tile q - 4.
-    // Lane l reads row R = 32 (q % 4) + l % 32, 16-byte segment 2 ks + l / 32
-    // (bf16) or 4 ks + 2 (l / 32) + piece (fp8).
-    constexpr int RPK = FP8 ? 16 : 8;
+    // (bf16) or r / 2 (fp8, piece r % 2); q < TM: A tile q, else W tile q - TM.
+    constexpr int RPK = 16;
     auto read_r = [&](int st, int ks, int r) {
         const int q = FP8 ? r >> 1 : r;
-        const int sgi = FP8 ? 4 * ks + 2 * (lane >> 5) + (r & 1) : 2 * ks + (lane >> 5);
-        const int off = st * kStage + ((sgi ^ fkey) << 4) + (q & 3) * 4096;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((q < 4 ? abase : bbase) + off);
+        const int sgi = FP8 ? 4 * ks + 2 * (lane >> 5) + (r & 1) : 4 * ks + (lane >> 4);
+        const int off = st * kStage + ((sgi ^ fkey) << 4) + (q % TM) * (TS * 128);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((q < TM ? abase : bbase) + off);
         if constexpr (FP8) {
-            Frag& fr = f[ks][q >> 2][q & 3];
+            Frag& fr = f[ks][q / TM][q % TM];
             const int h = 4 * (r & 1);
 #pragma unroll
             for (int w = 0; w < 4; ++w) fr[h + w] = v[w];
         } else {
-            f[ks][q >> 2][q & 3] = v;
+            f[ks][q / TM][q % TM] = v;
         }
     };
-    // MFMA m of k-step ks: slot tile m / 4, feature tile m % 4
+    // MFMA m of k-step ks: slot tile m / TM, feature tile m % TM
     auto mfma_one = [&](int ks, int m) {
-        const int i = m >> 2, j = m & 3;
+        const int i = m / TM, j = m % TM;
         if constexpr (FP8) {
             // formats 0, 0: fp8 e4m3 both; block scales 127: 2^0
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                 __builtin_bit_cast(i32x8_t, f[ks][1][j]), __builtin_bit_cast(i32x8_t, f[ks][0][i]), acc[i][j], 0, 0,
                 0, 127, 0, 127);
         } else {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f[ks][1][j]),
                                                                 __builtin_bit_cast(bf16x8_t, f[ks][0][i]),
                                                                 acc[i][j], 0, 0, 0);
         }
@@ -461,8 +493,8 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     setup_b(cur, co, 0u, buf);
     setup_scales(cur, buf);   // (older than the chunk loads below: their wait covers it)
     int par = 0;              // stage of chunk c: (c + par) & 1
-    // First tile: chunks 0 and 1 in flight, wait for chunk 0, read its
-    // k-steps 0..2.  Later tiles find theirs prefetched (below).
+    // First tile: chunks 0 and 1 in flight, wait for chunk 0, read its first
+    // k-step.  Later tiles find theirs prefetched (below).
     {
 #pragma unroll
         for (int q = 0; q < 16; ++q) dma_one(cur, co, buf, 0, par, q);
@@ -480,14 +512,14 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // next tile's chunks 0 and 1, so a tile starts with its data in LDS and the
     // previous tile's stores overlap its loads.
     const bool stream = nk >= 2;
-    // Step c (chunk c in stage (c + par) & 1, its k-steps 0..2 already in
+    // Step c (chunk c in stage (c + par) & 1, its first k-step already in
     // registers).  Each wave reads the chunk's last k-step, so once it has
     // waited for its reads and met the others, nobody reads that stage any
     // more: the stream's chunk two ahead is loaded into it (load(q), q < 16)
-    // while k-steps 1 and 2 multiply.  Then every wave waits for the stream's
-    // next chunk (the one after may stay in flight), meets the others, and
-    // reads its k-steps 0..2 under k-step 3's MFMAs -- within the tile; the
-    // next tile's first fragments are read after the epilogue.  Every load and
+    // while the next MFMAs run.  Then every wave waits for the stream's next
+    // chunk (the one after may stay in flight), meets the others, and reads
+    // its first k-step under the last MFMAs -- within the tile; the next
+    // tile's first fragments are read after the epilogue.  Every load and
     // fragment read sits between two MFMAs (the order is pinned): the matrix
     // pipe keeps a queued MFMA while they issue.
     auto step = [&](int c, auto load, bool more2, bool more1) {
@@ -495,11 +527,14 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         const int st1 = st ^ 1;                    // the stream's next chunk
         const bool rd1 = c + 1 < nk;
         if constexpr (!FP8) {
+            // 128 MFMAs (two k-steps of 64): k-step 1's 16 reads under the
+            // first 32, the 16 loads under the next 64 (one per four), the
+            // next chunk's k-step 0 under the last 32
 #pragma unroll
-            for (int m = 0; m < 16; ++m) {
+            for (int m = 0; m < 32; ++m) {
                 mfma_one(0, m);
                 pin();
-                if (m < 8) read_r(st, 3, m);
+                if (m & 1) read_r(st, 1, m >> 1);
                 pin();
             }
             // (the builtin, not inline assembly: the compiler then knows these
@@ -507,10 +542,10 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
             barrier();
 #pragma unroll
-            for (int m = 0; m < 32; ++m) {
-                mfma_one(1 + (m >> 4), m & 15);
+            for (int m = 32; m < 96; ++m) {
+                mfma_one(m >> 6, m & 63);
                 pin();
-                if (more2 && (m & 1)) load(m >> 1);
+                if (more2 && (m & 3) == 3) load((m - 32) >> 2);
                 pin();
             }
             if (more1) {
@@ -518,17 +553,14 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                 else dma_wait_barrier<0>();
             }
 #pragma unroll
-            for (int m = 0; m < 16; ++m) {
-                mfma_one(3, m);
+            for (int m = 96; m < 128; ++m) {
+                mfma_one(1, m & 63);
                 pin();
-                if (rd1) {
-                    const int r0 = (3 * m) / 2, r1 = (3 * m + 3) / 2;   // 24 reads over 16 MFMAs
-                    for (int r = r0; r < r1; ++r) read_r(st1, r >> 3, r & 7);
-                }
+                if (rd1 && (m & 1)) read_r(st1, 0, (m - 96) >> 1);
                 pin();
             }
         } else {
-            // Two k-steps of 16 MFMAs (each twice a bf16 MFMA's time), in the
+            // Two k-steps of 16 MFMAs (each twice a 32x32x16 bf16 MFMA's time), in the
             // same proportions: the last k-step's 16 reads under the first 8
             // MFMAs, the loads under the next 16, the next chunk's k-step 0
             // under the last 8.
@@ -591,20 +623,23 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             step(c, [&](int q) { dma_one(nxt, no, buf ^ 1, c + 2 - nk, par + nk, q); }, more_tiles,
                  c + 1 < nk || more_tiles);
 
-        // Epilogue straight from the accumulators: lane l holds slot (wm * 4 +
-        // i) * 32 + l % 32 and tile columns (wn * 4 + j) * 32 + 8 r + 4 (l / 32)
-        // + 0..3 in acc[i][j][4 r ..]; pairs of lanes swap halves so that each
-        // stores 16 bytes through a range-checked descriptor (rows past the
-        // tile's slots and columns past the output get an out-of-range offset
-        // and are dropped).  The
-        // LDS stages keep the next tile's chunks meanwhile.  The accumulators
-        // stay in the accumulation registers up to here (the epilogues'
-        // arithmetic would otherwise lead the register allocator to keep some
-        // in the vector registers the K loop needs).
+        // Epilogue straight from the accumulators.  bf16: lane l holds slot
+        // (wm * 8 + i) * 16 + l % 16 and tile columns (wn * 8 + j) * 16 +
+        // 4 (l / 16) + 0..3 in acc[i][j]; tiles j and j + 1 swap 16-lane rows
+        // (store_pair16).  fp8: lane l holds slot (wm * 4 + i) * 32 + l % 32
+        // and tile columns (wn * 4 + j) * 32 + 8 r + 4 (l / 32) + 0..3 in
+        // acc[i][j][4 r ..]; pairs of lanes swap halves (store_row_segment).
+        // Either way each lane stores 16 bytes through a range-checked
+        // descriptor (rows past the tile's slots and columns past the output
+        // get an out-of-range offset and are dropped).  The LDS stages keep
+        // the next tile's chunks meanwhile.  The accumulators stay in the
+        // accumulation registers up to here (the epilogues' arithmetic would
+        // otherwise lead the register allocator to keep some in the vector
+        // registers the K loop needs).
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
+            for (int j = 0; j < TM; ++j) asm volatile("" : "+a"(acc[i][j]));
         // fp8: the scale of slot tile i's row of a, and the weight-row scales
         // of 4 consecutive output columns, from the tile's copies in LDS
         // (wsbuf entry = output column of the tile; SwiGLU: gate column, or
@@ -654,26 +689,23 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                     }
                 }
             } else {
+            // gate tiles j = 0..3, up tiles j + 4; hidden wn * 64 + 16 j + ...
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < TM; ++i) {
                 __builtin_amdgcn_sched_barrier(0);       // one slot tile at a time: few temporaries
-                const int row = (wm * 4 + i) * 32 + r32;
+                const int row = (wm * TM + i) * TS + r16;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    u32x2_t P[4];
+                for (int j = 0; j < TM / 2; j += 2) {
+                    __builtin_amdgcn_sched_barrier(0);   // one pair of tiles at a time
+                    float h[8];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        __builtin_amdgcn_sched_barrier(0);   // one 4-value group at a time
-                        float h[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float gv = acc[i][j][4 * r + e];
-                            h[e] = (gv * sigmoid(gv)) * acc[i][j + 2][4 * r + e];
-                        }
-                        P[r] = u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                    for (int e = 0; e < 8; ++e) {
+                        const int jj = j + (e >> 2);
+                        const float gv = acc[i][jj][e & 3];
+                        h[e] = (gv * sigmoid(gv)) * acc[i][jj + TM / 2][e & 3];
                     }
-                    store_row_segment(P, cres, row < cur.rows, (uint32_t)row * (uint32_t)F,
-                                      cur.n0 + wn * 64 + j * 32, F, kh);
+                    store_pair16(h, cres, row < cur.rows, (uint32_t)row * (uint32_t)F, cur.n0 + wn * 64 + j * TS,
+                                 F, rho);
                 }
             }
             }
@@ -683,12 +715,12 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             // (the compiler barrier keeps the row-scale loads here rather than
             // hoisted above the K loop, where their registers would be live)
             asm volatile("" ::: "memory");
-            float sc[4];
+            float sc[TM];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < TM; ++i) {
                 sc[i] = 1.0f;
                 if constexpr (EPI == EPI_ROW_SCALE) {
-                    const int row = (wm * 4 + i) * 32 + r32;
+                    const int row = (wm * TM + i) * TS + (lane & (TS - 1));
                     sc[i] = g.row_scale[cur.s0 + min(row, cur.rows - 1)];
                 }
                 if constexpr (FP8) sc[i] = a_row_scale(i);
@@ -719,23 +751,20 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
                 }
             } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < TM; ++i) {
                 if constexpr (EPI == EPI_ROW_SCALE) __builtin_amdgcn_sched_barrier(0);   // one slot tile at a time
-                const int row = (wm * 4 + i) * 32 + r32;
+                const int row = (wm * TM + i) * TS + r16;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    __builtin_amdgcn_sched_barrier(0);       // one 32 x 32 tile at a time
-                    u32x2_t P[4];
+                for (int j = 0; j < TM; j += 2) {
+                    __builtin_amdgcn_sched_barrier(0);       // one pair of 16 x 16 tiles at a time
+                    float v[8];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float v[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            v[e] = EPI == EPI_ROW_SCALE ? sc[i] * acc[i][j][4 * r + e] : acc[i][j][4 * r + e];
-                        P[r] = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    for (int e = 0; e < 8; ++e) {
+                        const float a = acc[i][j + (e >> 2)][e & 3];
+                        v[e] = EPI == EPI_ROW_SCALE ? sc[i] * a : a;
                     }
-                    store_row_segment(P, cres, row < cur.rows, (uint32_t)row * (uint32_t)N,
-                                      cur.n0 + (wn * 4 + j) * 32, N, kh);
+                    store_pair16(v, cres, row < cur.rows, (uint32_t)row * (uint32_t)N, cur.n0 + (wn * TM + j) * TS,
+                                 N, rho);
                 }
             }
             }
@@ -744,9 +773,9 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
         // (nothing below moves into the epilogue, where it would hold registers)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+            for (int j = 0; j < TM; ++j) acc[i][j] = Acc{};
         if (!stream) {
             // one chunk per tile: load it now (every wave has finished reading
             // the stage: its reads were consumed by its MFMAs, and the
@@ -759,7 +788,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             dma_wait_barrier<0>();
         }
         // the next tile's chunk 0 is in its stage for every wave (the last
-        // step's wait and barrier, or the one just above): its k-steps 0..2
+        // step's wait and barrier, or the one just above): its first k-step
 #pragma unroll
         for (int r = 0; r < (NKS - 1) * RPK; ++r) read_r((par + nk) & 1, r / RPK, r % RPK);
         par = (par + nk) & 1;
