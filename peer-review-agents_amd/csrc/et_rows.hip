@@ -361,14 +361,15 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
     __syncthreads();
 }
 
-// Vector path, pass 1.  For every routed slot s and every 1 KiB piece p of
-// the row, one wave writes that piece of dYp[s] = gate[s] * dY[token(s)] and
-// the piece's partial dot <dY[t], Yp[s]> to part[s * npieces + p].  The
-// partial is formed in binary64: every product of two binary32 (or bf16)
-// values is exact in binary64, each lane sums its chunk's products in two fma
-// chains (even and odd elements, then added), and one DPP wave reduction sums
-// the lanes, so the partial carries about a dozen binary64 roundings.  Yp is
-// read once and dYp written once, both non-temporal.
+// Vector path, pass 1.  For every routed slot s and every pair q of 1 KiB
+// pieces of the row, one wave writes those pieces of dYp[s] = gate[s] *
+// dY[token(s)] and their partial dot <dY[t], Yp[s]> to part[s * nparts + q].
+// The partial is formed in binary64: every product of two binary32 (or bf16)
+// values is exact in binary64, each lane sums its 16 (bf16) or 8 (binary32)
+// products in two chains (even and odd elements, then added), and one DPP
+// wave reduction sums the lanes, so the partial carries about a dozen
+// binary64 roundings.  Yp is read once and dYp written once, both
+// non-temporal.
 //
 // Walk order.  Walking tokens (each token's ~k slots at once) has the waves in
 // flight touch a slot run in every expert block, each run visited again and
@@ -503,17 +504,12 @@ __global__ __launch_bounds__(kOrderThreads) void combine_bwd_order(
     }
 }
 
-template <int N>
-__device__ __forceinline__ double dot_f64(const double (&dd)[N], const float (&f)[N])
+// acc + a * b with the product exact: two binary32 (or bf16) values multiply
+// exactly in binary64 (24 + 24 significant bits, and no binary32 product
+// under- or overflows there), so the fma rounds once, at the addition.
+__device__ __forceinline__ double fma_exact(float a, float b, double acc)
 {
-    double a0 = dd[0] * (double)f[0];
-    double a1 = dd[1] * (double)f[1];
-#pragma unroll
-    for (int i = 2; i < N; i += 2) {
-        a0 = __builtin_fma(dd[i], (double)f[i], a0);
-        a1 = __builtin_fma(dd[i + 1], (double)f[i + 1], a1);
-    }
-    return a0 + a1;
+    return __builtin_fma((double)a, (double)b, acc);
 }
 
 // The main pass: one wave per (J, pair of pieces); both pieces' loads are
@@ -576,29 +572,30 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
                 wd[i] = ld16(dy + (int64_t)t * rb + idx[i] * 16);
             }
         }
+        // the wave's partial dot: even and odd elements of both pieces in two
+        // binary64 chains (an element past the row reads 0 from both rows)
+        double a0 = 0.0, a1 = 0.0;
 #pragma unroll
         for (int i = 0; i < kWinPieces; ++i) {
             float f[N], df[N], o[N];
-            double dd[N];
             P::unpack(wy[i], f);
             P::unpack(wd[i], df);
 #pragma unroll
-            for (int k = 0; k < N; ++k) {
-                dd[k] = (double)df[k];
-                o[k] = g * df[k];
-            }
+            for (int k = 0; k < N; ++k) o[k] = g * df[k];
             if (on[i]) st16_nt(dyp + (int64_t)s * rb + idx[i] * 16, P::pack(o));
-            const uint32_t p = q * kWinPieces + i;
-            if (p < npieces) {
-                const double dot = wave_sum_dpp_f64(dot_f64<N>(dd, f));
-                if (lane == 0) part[(int64_t)s * npieces + p] = dot;
+#pragma unroll
+            for (int k = 0; k < N; k += 2) {
+                a0 = fma_exact(df[k], f[k], a0);
+                a1 = fma_exact(df[k + 1], f[k + 1], a1);
             }
         }
+        const double dot = wave_sum_dpp_f64(a0 + a1);
+        if (lane == 0) part[(int64_t)s * nq + q] = dot;
     }
 }
 
 // Vector path, pass 2: one thread per slot s < min(expert_offsets[E], cap):
-// dgate[s] = the binary64 sum of the slot's partial dots in piece order,
+// dgate[s] = the binary64 sum of the slot's partial dots in order,
 // rounded once to binary32, and dlogits[sorted_token[s], e(s)] = dgate[s] *
 // (g * (1 - g)) in binary32, with e(s) found by a binary search of
 // expert_offsets in LDS.  A slot that pass 1 skipped (its
@@ -607,7 +604,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
 constexpr int kFinishThreads = 256;
 
 __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
-    const double* __restrict__ part, uint32_t npieces, const float* __restrict__ gate,
+    const double* __restrict__ part, uint32_t nparts, const float* __restrict__ gate,
     const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ tok_off,
     const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff, int E, int64_t cap,
     float* __restrict__ dgate, float* __restrict__ dlogits)
@@ -633,15 +630,15 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
             return;
         }
     }
-    const double* ps = part + s * npieces;
+    const double* ps = part + s * nparts;
     double acc = 0.0;
-    for (uint32_t q0 = 0; q0 < npieces; q0 += 8) {
+    for (uint32_t q0 = 0; q0 < nparts; q0 += 8) {
         double v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = ps[min(q0 + i, npieces - 1)];
+        for (int i = 0; i < 8; ++i) v[i] = ps[min(q0 + i, nparts - 1)];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (q0 + i < npieces) acc += v[i];
+            if (q0 + i < nparts) acc += v[i];
     }
     const float dot = (float)acc;
     dgate[s] = dot;
@@ -880,9 +877,15 @@ extern "C" int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offs
 
 static bool bwd_vector_path(int64_t d, int dtype) { return d > 0 && (d * elem_bytes(dtype)) % 16 == 0; }
 
-// Workspace of the vector path: the binary64 partial dots [cap * npieces],
+// Workspace of the vector path: the binary64 partial dots [cap * bwd_parts(np)],
 // then the slot order [cap] int32 at the next 256-byte boundary.
-static size_t bwd_order_offset(int64_t cap, int64_t np) { return ((size_t)(cap * np) * sizeof(double) + 255) & ~(size_t)255; }
+static size_t bwd_order_offset(int64_t cap, int64_t nparts)
+{
+    return ((size_t)(cap * nparts) * sizeof(double) + 255) & ~(size_t)255;
+}
+
+// Binary64 partial dots per slot: one per wave, i.e. per kWinPieces pieces.
+static int64_t bwd_parts(int64_t np) { return (np + kWinPieces - 1) / kWinPieces; }
 
 extern "C" size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype)
 {
@@ -890,7 +893,7 @@ extern "C" size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slo
     if (slot_capacity < 0 || d < 0 || (dtype != ET_DTYPE_F32 && dtype != ET_DTYPE_BF16)) return 0;
     if (!bwd_vector_path(d, dtype)) return 0;
     const int64_t np = (d * elem_bytes(dtype) / 16 + kWave - 1) / kWave;
-    return bwd_order_offset(slot_capacity, np) + (size_t)slot_capacity * 4;
+    return bwd_order_offset(slot_capacity, bwd_parts(np)) + (size_t)slot_capacity * 4;
 }
 
 extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_gate,
@@ -928,7 +931,7 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
         double* part = reinterpret_cast<double*>(wsb);
         int32_t* order = nullptr;
         if (cap > 0 && !bwd_slot_order(T, cap, rb)) {
-            order = reinterpret_cast<int32_t*>(wsb + bwd_order_offset(cap, np));
+            order = reinterpret_cast<int32_t*>(wsb + bwd_order_offset(cap, bwd_parts(np)));
             combine_bwd_order<<<dim3((unsigned)nw), dim3(kOrderThreads), (size_t)(3 * E + 1) * 4, s>>>(
                 token_offsets, token_slot, expert_offsets, (int)E, (int)T, (int)TW, cap, order);
             if (int rc = check_launch("combine_bwd_order")) return rc;
@@ -949,7 +952,7 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
         }
         if (cap == 0) return ET_OK;
         combine_bwd_finish<<<dim3((unsigned)((cap + kFinishThreads - 1) / kFinishThreads)), dim3(kFinishThreads),
-                             lds, s>>>(part, (uint32_t)np, slot_gate, sorted_token, token_offsets, token_slot,
+                             lds, s>>>(part, (uint32_t)bwd_parts(np), slot_gate, sorted_token, token_offsets, token_slot,
                                        expert_offsets, (int)E, cap, dgate, dlogits);
         return check_launch("combine_bwd_finish");
     }
