@@ -121,12 +121,14 @@ def test_error_string_is_per_call(et):
 
 def test_combine_bwd_workspace(et):
     lib = et.lib()
-    # one binary64 partial per slot and 1 KiB piece of the row (C3: d = 4096 bf16 -> 8
-    # pieces), then the slot walk order (one int32 per slot) from a 256-byte boundary
+    # one binary64 partial per slot and 2 KiB of the row (one wave's two 1 KiB pieces; C3:
+    # d = 4096 bf16 -> 4 partials; d = 512 f32 -> 1), then the slot walk order (one int32
+    # per slot) from a 256-byte boundary
     r = lambda x: (x + 255) // 256 * 256
-    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == r(528736 * 8 * 8) + 528736 * 4
-    assert lib.et_combine_bwd_workspace_bytes(4096, 8191, 512, 0) == r(8191 * 2 * 8) + 8191 * 4
-    assert lib.et_combine_bwd_workspace_bytes(1, 8191, 512, 0) == r(8191 * 2 * 8) + 8191 * 4
+    assert lib.et_combine_bwd_workspace_bytes(65536, 528736, 4096, 1) == r(528736 * 4 * 8) + 528736 * 4
+    assert lib.et_combine_bwd_workspace_bytes(4096, 8191, 512, 0) == r(8191 * 1 * 8) + 8191 * 4
+    assert lib.et_combine_bwd_workspace_bytes(1, 8191, 512, 0) == r(8191 * 1 * 8) + 8191 * 4
+    assert lib.et_combine_bwd_workspace_bytes(1, 100, 4104, 1) == r(100 * 5 * 8) + 100 * 4   # 9 pieces, 5 waves
     assert lib.et_combine_bwd_workspace_bytes(10, 100, 7, 1) == 0        # element path: none
     assert lib.et_combine_bwd_workspace_bytes(10, 100, 8, 5) == 0        # bad dtype
     p = ctypes.c_void_p(0x1000)                   # 16-byte aligned: the vector path is chosen
