@@ -10,8 +10,9 @@
 //     lane = expert (coalesced 256-byte row segments).  The first pass reads
 //     the logits, computes every score key once and stores the keys; the later
 //     passes read the keys.  A block counts the digits of the keys that match
-//     the prefix fixed so far in an LDS histogram and writes it whole to
-//     partial[group][block][lane][digit].
+//     the prefix fixed so far in an LDS histogram of 16-bit counts and writes
+//     it whole, two counts per word, to partial[group][block][lane][digit / 2]
+//     (digit d in the half d % 2).
 //   select: one block per expert sums the expert's partial histograms, finds
 //     the digit that holds the rank-th largest matching key, and narrows the
 //     prefix and the rank for the next pass.
@@ -31,9 +32,10 @@ constexpr int64_t kHistBlocksKeys = 256;    // blocks of the key passes (whole g
 constexpr int kHistUTKeys = 16;             // tokens in flight per wave, key passes
 constexpr int64_t kMaxTokensPerBlock = 65535;  // LDS counts are 16-bit
 constexpr int kPitch = kWave + 1;           // LDS words per digit pair (padded)
-constexpr int kHistSize = kWave * 256;      // counts in one block histogram
+constexpr int kHistWords = kWave * 128;     // words of one block histogram (two 16-bit counts each)
 constexpr int kSelectThreads = 1024;
-constexpr int kSelectSplit = kSelectThreads / 256;
+constexpr int kSelectSplit = kSelectThreads / 128;
+constexpr int kSelectRound = 8;             // partial-histogram loads in flight per select thread
 
 // Token blocks per 64-expert group of a histogram pass.
 struct HistGrid {
@@ -58,7 +60,7 @@ struct ThrWs {
     uint32_t* prefix;   // [E]  bits of the selected key fixed so far
     uint32_t* rank;     // [E]  rank still to find among keys matching prefix
     uint32_t* keys;     // [T * E] score keys (bit patterns of the scores; NaN -> 0)
-    uint32_t* partial;  // [groups][blocks][64][256] block histograms of one pass
+    uint32_t* partial;  // [groups][blocks][64][128] block histograms of one pass (16-bit counts, packed)
     HistGrid g1, g2;    // grids of the score pass and of the key passes
     size_t bytes;
 };
@@ -75,7 +77,7 @@ static ThrWs thr_ws_layout(void* base, int64_t T, int64_t E)
     ws.prefix = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(E) * 4);
     ws.rank = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(E) * 4);
     ws.keys = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(T * E) * 4);
-    ws.partial = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(groups * nb) * kHistSize * 4);
+    ws.partial = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(groups * nb) * kHistWords * 4);
     ws.bytes = off;
     return ws;
 }
@@ -128,17 +130,18 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
         }
     }
     __syncthreads();
-    uint32_t* out = partial + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kHistSize;
-    for (int i = tid; i < kHistSize; i += kHistThreads) {
-        const int l = i >> 8, d = i & 255;
-        out[i] = (h[(d >> 1) * kPitch + l] >> ((d & 1) * 16)) & 0xffffu;
+    uint32_t* out = partial + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kHistWords;
+    for (int i = tid; i < kHistWords; i += kHistThreads) {
+        const int l = i >> 7, j = i & 127;
+        out[i] = h[j * kPitch + l];
     }
 }
 
 // One block per expert: counts[d] = the sum of the expert's block histograms
-// (kSelectSplit threads per digit, each over every kSelectSplit-th block, all
-// loads of a round issued together), then one wave walks the digits from the
-// top to the one holding the rank-th largest matching key.
+// (kSelectSplit threads per word of two digits, each over every
+// kSelectSplit-th block, all loads of a round issued together; the two 16-bit
+// halves are added separately), then one wave walks the digits from the top to
+// the one holding the rank-th largest matching key.
 __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     int E, int shift, int nblocks, const uint32_t* __restrict__ partial, uint32_t* __restrict__ prefix,
     uint32_t* __restrict__ rank, uint32_t c0, float* __restrict__ thr, float* __restrict__ stat, float m)
@@ -146,17 +149,23 @@ __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     __shared__ uint32_t part[kSelectSplit][256];
     const int e = blockIdx.x;
     const int tid = threadIdx.x;
-    const int q = tid >> 8, d = tid & 255;
-    const uint32_t* src = partial + (int64_t)(e >> 6) * nblocks * kHistSize + (e & 63) * 256 + d;
-    uint32_t sum = 0u;
-    for (int b0 = q; b0 < nblocks; b0 += 8 * kSelectSplit) {
-        uint32_t v[8];
+    const int q = tid >> 7, j = tid & 127;
+    const uint32_t* src = partial + (int64_t)(e >> 6) * nblocks * kHistWords + (e & 63) * 128 + j;
+    uint32_t lo = 0u, hi = 0u;
+    for (int b0 = q; b0 < nblocks; b0 += kSelectRound * kSelectSplit) {
+        uint32_t v[kSelectRound];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = src[(int64_t)min(b0 + i * kSelectSplit, nblocks - 1) * kHistSize];
+        for (int i = 0; i < kSelectRound; ++i)
+            v[i] = src[(int64_t)min(b0 + i * kSelectSplit, nblocks - 1) * kHistWords];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sum += (b0 + i * kSelectSplit < nblocks) ? v[i] : 0u;
+        for (int i = 0; i < kSelectRound; ++i) {
+            const uint32_t w = (b0 + i * kSelectSplit < nblocks) ? v[i] : 0u;
+            lo += w & 0xffffu;
+            hi += w >> 16;
+        }
     }
-    part[q][d] = sum;
+    part[q][2 * j] = lo;
+    part[q][2 * j + 1] = hi;
     __syncthreads();
     if (tid >= kWave) return;
     const int lane = tid;
