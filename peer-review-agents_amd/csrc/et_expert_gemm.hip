@@ -87,9 +87,12 @@ constexpr int kKC = 64;           // k per chunk (four k-steps of 16): 128 bytes
 constexpr int kThreads = 256;
 // Slot tiles per group in the tile order: 8 for K >= 2048 (the gate/up
 // projections: 2.5-3% faster than 4 at C3 and C4), 4 below (the down
-// projection: 4.6% faster than 8 at C3).  The order changes no bits.
+// projection: 4.6% faster than 8 at C3), except 8 again when the experts with
+// slots average kGroupMBigExperts slot tiles or more (the down projection at
+// C4, 32 experts of 32 tiles: 2% faster with 8).  The order changes no bits.
 constexpr int kGroupMLargeK = 8;
 constexpr int kGroupMSmallK = 4;
+constexpr int kGroupMBigExperts = 24;
 constexpr int kHalf = 256 * 128;  // one operand's chunk: 256 rows x 128 bytes
 constexpr int kStage = 2 * kHalf; // A then W; two stages fill 128 KiB of LDS
 constexpr int kSmemBytes = 2 * kStage;
@@ -213,6 +216,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // the two operand stages
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
     __shared__ int ptile[ET_MAX_EXPERTS + 1];    // prefix of the per-expert slot-tile counts
+    __shared__ int nexp;                         // experts with at least one slot tile
     __shared__ int32_t tokbuf[2][kBM];           // gather: the tokens of a tile's slots, by tile parity
     // fp8: the weight-row scales of a tile's columns and the scales of its
     // rows of a, by tile parity (read as float4 in the epilogue)
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int E = g.E, K = g.K, N = g.N;
 
     if (wave == 0) {
-        int carry = 0;
+        int carry = 0, busy = 0;
         for (int e0 = 0; e0 < E; e0 += kWave) {
             const int e = e0 + lane;
             int n = 0;
@@ -237,8 +241,12 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
             const int inc = wave_incl_scan(n) + carry;
             if (e < E) ptile[e + 1] = inc;
             carry = __shfl(inc, kWave - 1, kWave);
+            busy += (int)__popcll(__ballot(n > 0));
         }
-        if (lane == 0) ptile[0] = 0;
+        if (lane == 0) {
+            ptile[0] = 0;
+            nexp = busy;
+        }
     }
     __syncthreads();
 
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     const int nN = EPI == EPI_SWIGLU ? (F + kBN / 2 - 1) / (kBN / 2) : (N + kBN - 1) / kBN;
     const int Q = ptile[E] * nN;
     const int per = (Q + 7) / 8;
-    const int group_m = K >= 2048 ? kGroupMLargeK : kGroupMSmallK;
+    const int group_m = (K >= 2048 || ptile[E] >= kGroupMBigExperts * nexp) ? kGroupMLargeK : kGroupMSmallK;
     const int nloc = (int)(gridDim.x / 8);
     const int xcd = (int)(blockIdx.x & 7);
     const int r32 = lane & 31;
