@@ -198,7 +198,8 @@ int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, const 
                            size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace et_threshold_update needs for T tokens and E experts
- * (it holds the T*E score keys and the radix-select histograms). */
+ * (it holds the T*E score keys, T*E candidate keys for the last digit and the
+ * radix-select histograms: about 8*T*E bytes). */
 size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 
 /*

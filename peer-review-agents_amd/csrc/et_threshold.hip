@@ -3,9 +3,14 @@
 // 8-bit MSB-first radix select over the score bits, then
 // thr[e] = fma(momentum, thr[e], (1 - momentum) * stat[e]).
 //
-// Four passes, one per 8-bit digit, each a histogram launch and a select
-// launch (the last select also applies the EMA); no global atomics, so the
-// result is deterministic by construction.
+// Three histogram passes and three select launches fix the top three 8-bit
+// digits; the third pass also copies out the keys that still match after two
+// digits (a few hundred per expert on C5-like data), and the last select
+// takes the fourth digit from those candidate lists in LDS, then applies the
+// EMA.  No pass uses a global atomic: a histogram block appends its
+// candidates to its own segment of the expert's list (an LDS counter per
+// expert gives the index), and only the segments' contents, not their order,
+// enter the result, so it is deterministic.
 //   histogram: grid (token blocks, 64-expert groups), 16 waves per block,
 //     lane = expert (coalesced 256-byte row segments).  The first pass reads
 //     the logits, computes every score key once and stores the keys; the later
@@ -15,7 +20,8 @@
 //     (digit d in the half d % 2).
 //   select: one block per expert sums the expert's partial histograms, finds
 //     the digit that holds the rank-th largest matching key, and narrows the
-//     prefix and the rank for the next pass.
+//     prefix and the rank for the next pass; the last one then histograms the
+//     expert's candidates by their lowest byte and fixes the statistic.
 #include <algorithm>
 
 #include "et_common.hpp"
@@ -61,6 +67,8 @@ struct ThrWs {
     uint32_t* rank;     // [E]  rank still to find among keys matching prefix
     uint32_t* keys;     // [T * E] score keys (bit patterns of the scores; NaN -> 0)
     uint32_t* partial;  // [groups][blocks][64][128] block histograms of one pass (16-bit counts, packed)
+    uint32_t* cand;     // [E][T] keys matching the two-digit prefix; block b's at [b * tpb, ...)
+    uint32_t* cand_n;   // [E][blocks] candidates of each block of the third pass
     HistGrid g1, g2;    // grids of the score pass and of the key passes
     size_t bytes;
 };
@@ -78,6 +86,8 @@ static ThrWs thr_ws_layout(void* base, int64_t T, int64_t E)
     ws.rank = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(E) * 4);
     ws.keys = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(T * E) * 4);
     ws.partial = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(groups * nb) * kHistWords * 4);
+    ws.cand = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(T * E) * 4);
+    ws.cand_n = reinterpret_cast<uint32_t*>(b + off); off += align256(size_t(E * ws.g2.blocks) * 4);
     ws.bytes = off;
     return ws;
 }
@@ -88,14 +98,21 @@ static ThrWs thr_ws_layout(void* base, int64_t T, int64_t E)
 // stored; otherwise the input is the stored keys.  LDS counts are 16-bit, two
 // digits to a word (word (d >> 1) * kPitch + lane, half d & 1); a block covers
 // at most 65535 tokens, so a half never carries into its neighbour.
-template <bool FIRST, int UT>
+// COMPACT (the third pass): every key that matches the two-digit prefix is
+// also stored in the block's segment of its expert's candidate list,
+// cand[e][t0 + i] for the block's tokens [t0, t1) (i from an LDS counter, so
+// i < t1 - t0), and the block's count goes to cand_n[e][block].
+template <bool FIRST, bool COMPACT, int UT>
 __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
     const float* __restrict__ logits, uint32_t* __restrict__ keys, int T, int E, int shift,
-    int tokens_per_block, const uint32_t* __restrict__ prefix, uint32_t* __restrict__ partial)
+    int tokens_per_block, const uint32_t* __restrict__ prefix, uint32_t* __restrict__ partial,
+    uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n)
 {
     __shared__ uint32_t h[128 * kPitch];
+    __shared__ uint32_t cn[kWave];
     const int tid = threadIdx.x;
     for (int i = tid; i < 128 * kPitch; i += kHistThreads) h[i] = 0u;
+    if (COMPACT && tid < kWave) cn[tid] = 0u;
     __syncthreads();
     const int lane = lane_id();
     const int wave = tid >> 6;
@@ -126,6 +143,10 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
             if ((key & hmask) == pre) {
                 const uint32_t d = (key >> shift) & 255u;
                 atomicAdd(&h[(d >> 1) * kPitch + lane], 1u << ((d & 1u) * 16));
+                if (COMPACT) {
+                    const uint32_t i = atomicAdd(&cn[lane], 1u);
+                    cand[(int64_t)e * T + t0 + i] = key;
+                }
             }
         }
     }
@@ -135,20 +156,66 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(
         const int l = i >> 7, j = i & 127;
         out[i] = h[j * kPitch + l];
     }
+    if (COMPACT && tid < kWave && ve) cand_n[(int64_t)e * gridDim.x + blockIdx.x] = cn[tid];
+}
+
+// Wave 0 of a select block: the bin of the rank-th largest key (rank r >= 1)
+// given the bin counts cnt(bin), bins walked from the top.  The lane that
+// holds it returns true with the bin and the rank left inside the bin.
+template <typename F>
+__device__ __forceinline__ bool find_digit(F cnt, int r, uint32_t& bin, int& rank_in)
+{
+    const int lane = lane_id();
+    // position p = 4*lane + i walks the bins from the top: bin = 255 - p
+    uint32_t c[4];
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c[i] = cnt(255 - (4 * lane + i));
+        tot += (int)c[i];
+    }
+    const int incl = wave_incl_scan(tot);
+    const int excl = incl - tot;
+    if (!(excl < r && r <= incl)) return false;
+    int run = excl;
+    int pos = 4 * lane + 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (run + (int)c[i] >= r) { pos = 4 * lane + i; break; }
+        run += (int)c[i];
+    }
+    bin = 255u - (uint32_t)pos;
+    rank_in = r - run;
+    return true;
 }
 
 // One block per expert: counts[d] = the sum of the expert's block histograms
 // (kSelectSplit threads per word of two digits, each over every
 // kSelectSplit-th block, all loads of a round issued together; the two 16-bit
-// halves are added separately), then one wave walks the digits from the top to
-// the one holding the rank-th largest matching key.
+// halves are added separately), then wave 0 finds the digit that holds the
+// rank-th largest matching key.  FINAL (the third select, shift 8): the digit
+// found fixes 24 bits; the block then counts the lowest byte of the expert's
+// candidates that match them (LDS histogram), wave 0 finds the last digit,
+// and the statistic goes into the EMA.  The candidate segments are taken up
+// to kSelectThreads blocks at a time: a block-wide scan of their counts
+// places them, and thread i of a round finds its segment by binary search.
+template <bool FINAL>
 __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     int E, int shift, int nblocks, const uint32_t* __restrict__ partial, uint32_t* __restrict__ prefix,
-    uint32_t* __restrict__ rank, uint32_t c0, float* __restrict__ thr, float* __restrict__ stat, float m)
+    uint32_t* __restrict__ rank, uint32_t c0, float* __restrict__ thr, float* __restrict__ stat, float m,
+    const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_n, int T, int tpb)
 {
     __shared__ uint32_t part[kSelectSplit][256];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t seg_end[kSelectThreads];  // FINAL: inclusive scan of a round's segment counts
+    __shared__ uint32_t wsum[kSelectThreads / kWave];
+    __shared__ uint32_t sel[2];                  // FINAL: the 24-bit prefix and the rank inside it
     const int e = blockIdx.x;
     const int tid = threadIdx.x;
+    if (FINAL) {
+        if (tid < 256) hist[tid] = 0u;
+        if (tid == 0) { sel[0] = 0xffffffffu; sel[1] = 0u; }
+    }
     const int q = tid >> 7, j = tid & 127;
     const uint32_t* src = partial + (int64_t)(e >> 6) * nblocks * kHistWords + (e & 63) * 128 + j;
     uint32_t lo = 0u, hi = 0u;
@@ -167,43 +234,72 @@ __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     part[q][2 * j] = lo;
     part[q][2 * j + 1] = hi;
     __syncthreads();
-    if (tid >= kWave) return;
-    const int lane = tid;
-    // position p = 4*lane + i walks the bins from the top: bin = 255 - p
-    uint32_t c[4];
-    int tot = 0;
+    auto pass_count = [&](int bin) {
+        uint32_t c = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int bin = 255 - (4 * lane + i);
-        c[i] = 0u;
-#pragma unroll
-        for (int k = 0; k < kSelectSplit; ++k) c[i] += part[k][bin];
-        tot += (int)c[i];
+        for (int k = 0; k < kSelectSplit; ++k) c += part[k][bin];
+        return c;
+    };
+    if (!FINAL) {
+        if (tid >= kWave) return;
+        // the first pass starts from the empty prefix and rank c0
+        const bool first = shift == 24;
+        uint32_t bin;
+        int rin;
+        if (find_digit(pass_count, first ? (int)c0 : (int)rank[e], bin, rin)) {
+            prefix[e] = (first ? 0u : prefix[e]) | (bin << shift);
+            rank[e] = (uint32_t)rin;
+        }
+        return;
     }
-    const int incl = wave_incl_scan(tot);
-    const int excl = incl - tot;
-    // the first pass starts from the empty prefix and rank c0
-    const bool first = shift == 24;
-    const int r = first ? (int)c0 : (int)rank[e];
-    if (excl < r && r <= incl) {
-        int run = excl;
-        int pos = 4 * lane + 3;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (run + (int)c[i] >= r) { pos = 4 * lane + i; break; }
-            run += (int)c[i];
+    if (tid < kWave) {
+        uint32_t bin;
+        int rin;
+        if (find_digit(pass_count, (int)rank[e], bin, rin)) {
+            sel[0] = prefix[e] | (bin << 8);
+            sel[1] = (uint32_t)rin;
         }
-        const uint32_t bin = 255u - (uint32_t)pos;
-        const uint32_t p = (first ? 0u : prefix[e]) | (bin << shift);
+    }
+    __syncthreads();
+    const uint32_t p24 = sel[0];
+    const uint32_t* cl = cand + (int64_t)e * T;
+    const uint32_t* cnt = cand_n + (int64_t)e * nblocks;
+    const int wave = tid >> 6;
+    for (int b0 = 0; b0 < nblocks; b0 += kSelectThreads) {
+        const int nc = min(kSelectThreads, nblocks - b0);
+        const uint32_t n = tid < nc ? cnt[b0 + tid] : 0u;
+        const uint32_t incl = (uint32_t)wave_incl_scan((int)n);
+        if (lane_id() == kWave - 1) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t below = 0u;
+        for (int w = 0; w < wave; ++w) below += wsum[w];
+        seg_end[tid] = below + incl;
+        __syncthreads();
+        const uint32_t total = seg_end[nc - 1];
+        for (uint32_t i = tid; i < total; i += kSelectThreads) {
+            int lo = 0, hi = nc - 1;                 // the first segment that ends past i
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (seg_end[mid] > i) hi = mid; else lo = mid + 1;
+            }
+            const uint32_t start = lo ? seg_end[lo - 1] : 0u;
+            const uint32_t key = cl[(int64_t)(b0 + lo) * tpb + (i - start)];
+            if ((key & 0xffffff00u) == p24) atomicAdd(&hist[key & 255u], 1u);
+        }
+        __syncthreads();
+    }
+    if (tid >= kWave) return;
+    uint32_t bin;
+    int rin;
+    if (find_digit([&](int b) { return hist[b]; }, (int)sel[1], bin, rin)) {
+        const uint32_t p = p24 | bin;
         prefix[e] = p;
-        rank[e] = (uint32_t)(r - run);
-        if (shift == 0) {
-            // the last pass fixed every bit: p is the statistic; apply the EMA
-            const float st = u2f(p);
-            if (stat) stat[e] = st;
-            const float one_minus_m = 1.0f - m;
-            thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
-        }
+        rank[e] = (uint32_t)rin;
+        // every bit is fixed: p is the statistic; apply the EMA
+        const float st = u2f(p);
+        if (stat) stat[e] = st;
+        const float one_minus_m = 1.0f - m;
+        thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
     }
 }
 
@@ -246,20 +342,28 @@ extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, i
     const int Ti = (int)T, Ei = (int)E;
     const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
 
-    for (int pass = 0; pass < 4; ++pass) {
+    for (int pass = 0; pass < 3; ++pass) {
         const int shift = 24 - 8 * pass;
         const HistGrid& g = pass == 0 ? ws.g1 : ws.g2;
         const dim3 grid((unsigned)g.blocks, groups);
         if (pass == 0)
-            thr_hist_kernel<true, kHistUTFirst><<<grid, dim3(kHistThreads), 0, s>>>(
-                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial);
+            thr_hist_kernel<true, false, kHistUTFirst><<<grid, dim3(kHistThreads), 0, s>>>(
+                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial, ws.cand, ws.cand_n);
+        else if (pass == 1)
+            thr_hist_kernel<false, false, kHistUTKeys><<<grid, dim3(kHistThreads), 0, s>>>(
+                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial, ws.cand, ws.cand_n);
         else
-            thr_hist_kernel<false, kHistUTKeys><<<grid, dim3(kHistThreads), 0, s>>>(
-                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial);
+            thr_hist_kernel<false, true, kHistUTKeys><<<grid, dim3(kHistThreads), 0, s>>>(
+                logits, ws.keys, Ti, Ei, shift, (int)g.tpb, ws.prefix, ws.partial, ws.cand, ws.cand_n);
         if (int rc = check_launch("thr_hist_kernel")) return rc;
-        thr_select_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(Ei, shift, (int)g.blocks, ws.partial,
-                                                                   ws.prefix, ws.rank, (uint32_t)c, thr, stat,
-                                                                   momentum);
+        if (pass < 2)
+            thr_select_kernel<false><<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(
+                Ei, shift, (int)g.blocks, ws.partial, ws.prefix, ws.rank, (uint32_t)c, thr, stat, momentum, ws.cand,
+                ws.cand_n, Ti, (int)ws.g2.tpb);
+        else
+            thr_select_kernel<true><<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(
+                Ei, shift, (int)g.blocks, ws.partial, ws.prefix, ws.rank, (uint32_t)c, thr, stat, momentum, ws.cand,
+                ws.cand_n, Ti, (int)ws.g2.tpb);
         if (int rc = check_launch("thr_select_kernel")) return rc;
     }
     return ET_OK;

@@ -353,6 +353,24 @@ def test_threshold_update_bit_exact(et, orc, dev, T, E, k):
     np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
 
 
+@pytest.mark.parametrize("T,E,k", [(70000, 72, 5), (3000, 64, 64)])
+def test_threshold_update_ties(et, orc, dev, T, E, k):
+    """Columns of a few distinct values, one all-NaN column and one constant
+    column: the c-th largest key sits in a run of equal keys, and a column's
+    keys can all share their top 24 bits."""
+    rng = np.random.default_rng([T, E, 1])
+    lg = rng.integers(-2, 2, (T, E)).astype(np.float32) * 0.5
+    lg[:, 3] = np.nan
+    lg[:, 5] = 1.25
+    lg[rng.random((T, E)) < 0.01] = np.nan
+    thr0 = rng.random(E).astype(np.float32)
+    thr_o, stat_o = orc.threshold_update(lg, thr0, k, 0.9)
+    thr = dev_f32(thr0, dev)
+    stat = et.threshold_update_(thr, dev_f32(lg, dev), k, 0.9)
+    np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+    np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
+
+
 def test_threshold_dynamics_c5(et, orc, dev):
     """C5 at reduced T: 100 routing steps on fresh logits, EMA after each."""
     cfg = W.CONFIGS["C5"]
