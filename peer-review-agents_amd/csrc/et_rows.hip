@@ -611,17 +611,26 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
 {
     extern __shared__ int32_t eo[];                                     // [E + 1]
     const bool want_dl = dlogits != nullptr;
+    const int64_t s = (int64_t)blockIdx.x * kFinishThreads + threadIdx.x;
+    // The slot's loads depend on s only: issue them (clamped below the
+    // capacity, every array holds cap slots) before the expert offsets land.
+    const int64_t sc = min(s, cap - 1);
+    const double* ps = part + sc * nparts;
+    double v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ps[min((uint32_t)i, nparts - 1)];
+    const float g = gate[sc];
+    const int t = sorted_token[sc];
+    const int64_t routed = eoff[E];
     if (want_dl)
         for (int e = threadIdx.x; e <= E; e += kFinishThreads) eo[e] = eoff[e];
     __syncthreads();
-    const int64_t s = (int64_t)blockIdx.x * kFinishThreads + threadIdx.x;
-    const int64_t S = min((int64_t)eoff[E], cap);
+    const int64_t S = min(routed, cap);
     if (s >= S) return;
-    if ((int64_t)eoff[E] > cap) {
+    if (routed > cap) {
         // Undersized capacity: pass 1 skipped slot s unless its token-list
         // entry is also below the capacity.  Only the token whose list
         // straddles the capacity needs a search.
-        const int t = sorted_token[s];
         const int64_t a = max(tok_off[t], 0), b = tok_off[t + 1];
         bool kept = b <= cap;
         for (int64_t j = a; !kept && j < cap && j < b; ++j) kept = tok_slot[j] == (int32_t)s;
@@ -630,10 +639,11 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
             return;
         }
     }
-    const double* ps = part + s * nparts;
     double acc = 0.0;
-    for (uint32_t q0 = 0; q0 < nparts; q0 += 8) {
-        double v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if ((uint32_t)i < nparts) acc += v[i];
+    for (uint32_t q0 = 8; q0 < nparts; q0 += 8) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = ps[min(q0 + i, nparts - 1)];
 #pragma unroll
@@ -644,8 +654,7 @@ __global__ __launch_bounds__(kFinishThreads) void combine_bwd_finish(
     dgate[s] = dot;
     if (want_dl) {
         const int e = expert_of_slot(eo, E, (int)s);
-        const float g = gate[s];
-        dlogits[(int64_t)sorted_token[s] * E + e] = dot * (g * (1.0f - g));
+        dlogits[(int64_t)t * E + e] = dot * (g * (1.0f - g));
     }
 }
 
