@@ -126,6 +126,30 @@ def test_threshold_dynamics_c5_full_size_100_steps(et, orc, dev):
     assert float(thr_o.max()) < cfg["thr0"]
 
 
+def test_threshold_update_many_blocks(et, orc, dev):
+    """T = 68,000,000 tokens: the histogram passes need more than 1024 token
+    blocks (a block counts at most 65,535 tokens in 16-bit LDS counts), so the
+    last select takes the candidate segments in two rounds.  E = 2, k = 1: the
+    statistic is the median.  Column 0 holds six distinct logits, so the
+    median sits in a run of millions of equal keys (every one a candidate);
+    column 1 is normal.  Statistic and thresholds bit-exact with the oracle."""
+    from test_gpu_parity import bits
+
+    T, E = 68_000_000, 2
+    rng = np.random.default_rng(11)
+    lg = np.empty((T, E), np.float32)
+    lg[:, 0] = rng.integers(-3, 3, T, dtype=np.int8).astype(np.float32) * 0.75
+    lg[:, 1] = rng.standard_normal(T, dtype=np.float32)
+    lg[::97, 1] = np.nan
+    thr0 = np.array([0.3, 0.7], np.float32)
+    thr = dev_f32(thr0, dev)
+    print(f"threshold update T={T} E={E}", flush=True)
+    stat = et.threshold_update_(thr, dev_f32(lg, dev), 1, 0.9)
+    thr_o, stat_o = orc.threshold_update(lg, thr0, 1, 0.9)
+    np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+    np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
+
+
 @pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
 def test_rows_full_size_against_oracle(et, orc, dev, name):
     """Every configuration at its full size against the CPU oracle itself
