@@ -1,20 +1,29 @@
 // et_router.hip -- the router producer of the path on gfx950: router logits
 // L[T, E] (f32) = X[T, d] (bf16) * W[E, d]^T (bf16), binary32 accumulation on
-// the MFMA units (v_mfma_f32_32x32x16_bf16).
+// the MFMA units (v_mfma_f32_16x16x32_bf16 up to 128 experts,
+// v_mfma_f32_32x32x16_bf16 above).
 //
 // The GEMM is skinny (E <= 256 columns) and HBM-bound on X: X is read from HBM
 // exactly once, W (E * d * 2 bytes) stays in L2 and is staged through LDS.
 //
-// Tiling: a block of MW waves owns 32 * MW tokens (32 per wave) and all E
-// experts (NT tiles of 32).  The K dimension advances in chunks of KC: the
-// block copies W[:, chunk] into LDS (double-buffered, one barrier per chunk)
-// while every wave loads its own X fragments straight from global memory,
-// several chunks ahead; each k-step of 16 is one MFMA per expert tile.
+// Tiling: a block of MW waves owns 32 * MT * MW tokens (32 * MT per wave)
+// and all E experts (NT groups of 32).  The K dimension advances in chunks of
+// KC: the block copies W[:, chunk] into LDS (double-buffered, one barrier per
+// chunk) while every wave loads its own X fragments straight from global
+// memory, several chunks ahead; each k-step is one MFMA per token tile and
+// expert tile.
 //
-// MFMA 32x32x16 bf16 operand layout (checked on the device): lane l holds
-//   A: row l % 32, k = 8 * (l / 32) + i, i < 8     -> 16 contiguous bytes of X
-//   B: col l % 32, k = 8 * (l / 32) + i            -> 16 contiguous bytes of W
-//   C: col l % 32, acc[j] at row 8 * (j / 4) + 4 * (l / 32) + j % 4
+// MFMA operand layouts (M x M tiles, M = 16 or 32): lane l holds
+//   A: row l % M, k = 8 * (l / M) + i, i < 8      -> 16 contiguous bytes of X
+//   B: col l % M, k = 8 * (l / M) + i             -> 16 contiguous bytes of W
+//   C, M = 16 (k-step 32): col l % 16, acc[j] at row 4 * (l / 16) + j
+//   C, M = 32 (k-step 16): col l % 32, acc[j] at row 8 * (j / 4) + 4 * (l / 32) + j % 4
+// With M = 16 one X load covers 16 rows x 64 contiguous bytes instead of 32
+// rows x 32 bytes, which streams faster.  On gfx950 the 16x16x32 result
+// equals two 16-k steps rounded in turn, so both forms give the same bits
+// (the k-order test checks the order).  With more than 128 experts the
+// 16 x 16 form's B fragments of a k-step and two token tiles per wave no
+// longer fit beside the accumulators, and the 32 x 32 form is kept.
 #include <algorithm>
 
 #include "et_common.hpp"
@@ -23,6 +32,7 @@
 namespace et {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -37,11 +47,47 @@ constexpr uint32_t kBufOutOfRange = 0x80000000u;
 // of the MFMAs).  KC is the k per chunk; the double-buffered W chunk in LDS is
 // 2 * NT * 32 rows * (KC + 8) bf16 (rows padded by 16 bytes so that the B
 // fragment reads are free of bank conflicts).
+// The two MFMA forms: tile size M, k per MFMA, and the token row (within the
+// tile) of accumulator element j of a lane.
+template <int M> struct RtMfma;
+template <> struct RtMfma<16> {
+    static constexpr int KS = 32;
+    static constexpr int NACC = 4;
+    typedef f32x4_t Acc;
+    static __device__ __forceinline__ Acc mma(u32x4_t a, u32x4_t b, Acc c)
+    {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ int crow(int lane, int j) { return 4 * (lane >> 4) + j; }
+    // 16-token route group (within the wave) of element j of token tile m
+    static constexpr int group(int m, int j) { return m; }
+};
+template <> struct RtMfma<32> {
+    static constexpr int KS = 16;
+    static constexpr int NACC = 16;
+    typedef f32x16_t Acc;
+    static __device__ __forceinline__ Acc mma(u32x4_t a, u32x4_t b, Acc c)
+    {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ int crow(int lane, int j) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
+    static constexpr int group(int m, int j) { return 2 * m + j / 8; }
+};
+
 template <int NT, int MW, int MT, int R> struct RtShape {
     static constexpr int THREADS = MW * kWave;
+    static constexpr int M = NT <= 4 ? 16 : 32;   // MFMA tile
+    using F = RtMfma<M>;
     static constexpr int KC = NT <= 4 ? 64 : 32;
     static constexpr int PITCH = KC + 8;        // bf16 per LDS row
-    static constexpr int KSTEPS = KC / 16;
+    static constexpr int KSTEPS = KC / F::KS;   // MFMA k-steps per chunk
+    static constexpr int TT = 32 * MT / M;      // token tiles per wave
+    static constexpr int ET = 32 * NT / M;      // expert tiles
+    // B fragments are read in units of ET / UPS tiles, double-buffered
+    // (unit u + 1 under unit u's MFMAs)
+    static constexpr int UPS = M == 16 ? 2 : 1;
     static constexpr int PF = R - 1;
     static constexpr int TOK = MW * MT * 32;    // tokens per block tile
     static constexpr int SEGS = NT * 32 * KC / 8;  // 16-byte W segments per chunk
@@ -69,21 +115,19 @@ struct RouteEpilogue {
 // exact scores.  So the selection, gates and argmax fallback are those of
 // et_route (select_token) bit for bit, with far fewer sigmoids: gates are
 // computed only for the routed pairs, after each 16-token group.
-// acc[m][n][j] is the logit of token t0 + 32 m + r, r = 8 (j / 4) +
-// 4 (lane / 32) + j % 4, expert 32 n + lane % 32.  The waves run through it
+// acc[m][n][j] is the logit of token t0 + M m + crow(lane, j), expert
+// M n + lane % M.  The waves run through it
 // independently; the tile sums at the end take two block barriers (`red`
 // aliases the W buffer, which every wave has finished reading once the K
 // loop's last barrier has passed).
-template <int NT, int MW, int MT>
-__device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], const RouteEpilogue& ro,
+template <int NT, int MW, int MT, typename S>
+__device__ __forceinline__ void route_epilogue(const typename S::F::Acc (&acc)[S::TT][S::ET], const RouteEpilogue& ro,
                                                float* rbuf, int* red, int tile, int wave, int64_t t0, int T, int E)
 {
-    constexpr int P = NT * 32 + 8;              // LDS row pitch (floats): both halves' writes on distinct banks
+    constexpr int P = NT * 32 + 8;              // LDS row pitch (floats)
     constexpr int GM = (NT * 32 + kWave - 1) / kWave;
     constexpr int DUMMY = 16 * P - 1;           // padding of the last row: never a logit, never a list entry
     const int lane = lane_id();
-    const int half = lane >> 5;
-    const int row = lane & 31;
     const int G = (E + kWave - 1) / kWave;
     const int nwords = (E + 31) / 32;
     float th[GM], hi[GM], lo[GM];
@@ -94,24 +138,25 @@ __device__ __forceinline__ void route_epilogue(const f32x16_t (&acc)[MT][NT], co
 #pragma unroll
     for (int g = 0; g < GM; ++g) wcnt[g] = 0;
     int wslots = 0;
+    using F = typename S::F;
+    constexpr int M = S::M;
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
+    for (int gi = 0; gi < 2 * MT; ++gi) {
+        {
+            // the 16 tokens of route group gi, one row of rbuf each
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            // tokens 16 hh .. 16 hh + 15 of token tile m <- j = 8 hh .. 8 hh + 7
+            for (int m = 0; m < S::TT; ++m)
 #pragma unroll
-            for (int n = 0; n < NT; ++n)
+                for (int n = 0; n < S::ET; ++n)
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int j = 8 * hh + jj;
-                    const int u = 8 * (jj / 4) + 4 * half + (j % 4);
-                    rbuf[u * P + n * 32 + row] = acc[m][n][j];
-                }
+                    for (int j = 0; j < F::NACC; ++j)
+                        if (F::group(m, j) == gi)
+                            rbuf[((m * M + F::crow(lane, j)) & 15) * P + n * M + (lane & (M - 1))] = acc[m][n][j];
             // rbuf is private to this wave and a wave's LDS operations run in
             // issue order, so the fences only have to keep the compiler from
             // moving these accesses across each other.
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            const int64_t tg = t0 + m * 32 + 16 * hh;     // first token of the route group
+            const int64_t tg = t0 + gi * 16;               // first token of the route group
             const int64_t q = tg / 16;
             const int nu = (int)std::min<int64_t>(16, std::max<int64_t>(0, (int64_t)T - tg));
             // Stores go through range-checked buffer descriptors: a lane with
@@ -248,8 +293,10 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int half = lane >> 5;            // which 8 of a k-step's 16
-    const int row = lane & 31;
+    using F = typename S::F;
+    constexpr int M = S::M;
+    const int quad = lane / M;             // which 8 k of a k-step
+    const int row = lane & (M - 1);
     const int nchunks = (d + S::KC - 1) / S::KC;
     const int ntiles = (int)((T + S::TOK - 1) / S::TOK);
     // Buffer loads with the hardware range check: an offset at or past a
@@ -299,24 +346,24 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
                 }
             }
         };
-        u32x4_t xr[R][MT][S::KSTEPS];
-        auto load_x = [&](int c, u32x4_t (&a)[MT][S::KSTEPS]) {
+        u32x4_t xr[R][S::TT][S::KSTEPS];
+        auto load_x = [&](int c, u32x4_t (&a)[S::TT][S::KSTEPS]) {
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
+            for (int m = 0; m < S::TT; ++m)
 #pragma unroll
                 for (int s = 0; s < S::KSTEPS; ++s) {
-                    const int k = chunk_at(c) * S::KC + s * 16 + half * 8;
+                    const int k = chunk_at(c) * S::KC + s * F::KS + quad * 8;
                     const uint32_t off =
-                        k < d ? (uint32_t)(m * 32 + row) * (uint32_t)d * 2u + (uint32_t)k * 2u : kBufOutOfRange;
+                        k < d ? (uint32_t)(m * M + row) * (uint32_t)d * 2u + (uint32_t)k * 2u : kBufOutOfRange;
                     a[m][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
                 }
         };
 
-        f32x16_t acc[MT][NT];
+        typename F::Acc acc[S::TT][S::ET];
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < S::TT; ++m)
 #pragma unroll
-            for (int n = 0; n < NT; ++n) acc[m][n] = f32x16_t{};
+            for (int n = 0; n < S::ET; ++n) acc[m][n] = typename F::Acc{};
 
         // prologue: W chunk 0 -> LDS, W chunk 1 -> wreg[1], X chunks 0 .. PF-1
         load_w(0, wreg[0]);
@@ -338,25 +385,28 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             __builtin_amdgcn_sched_barrier(0);
             load_x(c + S::PF, xr[(r + S::PF) % R]);
             __builtin_amdgcn_sched_barrier(0);
+            constexpr int UT = S::ET / S::UPS;       // expert tiles per unit
+            constexpr int NU = S::UPS * S::KSTEPS;
             const uint16_t* wb = wl[r & 1];
-            u32x4_t bf[2][NT];
-            auto rdb = [&](int s, int b) {
+            u32x4_t bf[2][UT];
+            auto rdb = [&](int u, int b) {
+                const int n0 = (u % S::UPS) * UT, s = u / S::UPS;
 #pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    bf[b][n] = *reinterpret_cast<const u32x4_t*>(&wb[(n * 32 + row) * S::PITCH + s * 16 + half * 8]);
+                for (int n = 0; n < UT; ++n)
+                    bf[b][n] = *reinterpret_cast<const u32x4_t*>(
+                        &wb[((n0 + n) * M + row) * S::PITCH + s * F::KS + quad * 8]);
             };
             rdb(0, 0);
 #pragma unroll
-            for (int s = 0; s < S::KSTEPS; ++s) {
-                if (s + 1 < S::KSTEPS) rdb(s + 1, (s + 1) & 1);
+            for (int u = 0; u < NU; ++u) {
+                if (u + 1 < NU) rdb(u + 1, (u + 1) & 1);
                 __builtin_amdgcn_sched_barrier(0);
+                const int n0 = (u % S::UPS) * UT, s = u / S::UPS;
 #pragma unroll
-                for (int n = 0; n < NT; ++n)
+                for (int n = 0; n < UT; ++n)
 #pragma unroll
-                    for (int m = 0; m < MT; ++m)
-                        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            __builtin_bit_cast(bf16x8_t, xr[r][m][s]), __builtin_bit_cast(bf16x8_t, bf[s & 1][n]),
-                            acc[m][n], 0, 0, 0);
+                    for (int m = 0; m < S::TT; ++m)
+                        acc[m][n0 + n] = F::mma(xr[r][m][s], bf[u & 1][n], acc[m][n0 + n]);
                 __builtin_amdgcn_sched_barrier(0);
             }
             store_w((r + 1) & 1, wreg[(r + 1) & 1]);
@@ -374,28 +424,27 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
         for (int r = 0; r < R - 1; ++r)
             if (nmain + r < nchunks) step(nmain + r, r);
 
-        // epilogue: lane l writes expert n * 32 + l % 32 of 16 token rows per tile
+        // epilogue: lane l writes expert n * M + l % M of its token rows per tile
         if (!ROUTE || logits != nullptr) {
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
+            for (int m = 0; m < S::TT; ++m)
 #pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    const int e = n * 32 + row;
+                for (int n = 0; n < S::ET; ++n) {
+                    const int e = n * M + row;
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const int64_t t = t0 + m * 32 + 8 * (j / 4) + 4 * half + (j % 4);
+                    for (int j = 0; j < F::NACC; ++j) {
+                        const int64_t t = t0 + m * M + F::crow(lane, j);
                         if (t < T && e < E) logits[t * E + e] = acc[m][n][j];
                     }
                 }
         }
         if constexpr (ROUTE)
-            route_epilogue<NT, MW, MT>(acc, ro, rbuf + wave * 16 * (NT * 32 + 8), reinterpret_cast<int*>(wl[0]), tile,
+            route_epilogue<NT, MW, MT, S>(acc, ro, rbuf + wave * 16 * (NT * 32 + 8), reinterpret_cast<int*>(wl[0]), tile,
                                        wave, t0, T, E);
     }
 }
 
-// X ring length: 8-16 KiB of X in flight per wave (with 8 expert tiles and
-// two token tiles the accumulators alone take 256 registers).
+// X ring length: 8-16 KiB of X in flight per wave.
 template <int NT, int MT> constexpr int kRouterRing = NT <= 4 ? 4 / MT : 4;
 
 template <int NT, int MW, int MT, bool ROUTE>
