@@ -21,7 +21,7 @@
 // With M = 16 one X load covers 16 rows x 64 contiguous bytes instead of 32
 // rows x 32 bytes, which streams faster.  On gfx950 the 16x16x32 result
 // equals two 16-k steps rounded in turn, so both forms give the same bits
-// (the k-order test checks the order).  With more than 128 experts the
+// (tests/test_gpu_router.py checks the rounding and the k order).  With more than 128 experts the
 // 16 x 16 form's B fragments of a k-step and two token tiles per wave no
 // longer fit beside the accumulators, and the 32 x 32 form is kept.
 #include <algorithm>

@@ -88,6 +88,24 @@ def test_router_logits_k_order(et, dev, T, E):
     assert torch.equal(L.double(), want[:, None].expand(T, E))
 
 
+@pytest.mark.parametrize("T,E", [(2048, 16), (2048, 200), (66000, 128), (66000, 256)])
+def test_router_logits_rounds_every_16_k(et, dev, T, E):
+    """Each logit is rounded after every k-step of 16, also where one MFMA
+    covers 32 k (up to 128 experts).  x = 2^24 at k = 0, 1 at k = 1 and 1 at
+    k = 16, w = 1: rounding after k 0..15 gives 2^24 (the tie 2^24 + 1 goes to
+    even), and adding the second 1 rounds away again, so every logit is 2^24
+    from any start of the k walk; one rounding over k 0..31 would give 2^24 + 2."""
+    print(f"router_logits 16-k rounding T={T} E={E}", flush=True)
+    d = 512
+    x = torch.zeros(T, d, device=dev, dtype=torch.bfloat16)
+    x[:, 0] = 2.0 ** 24
+    x[:, 1] = 1.0
+    x[:, 16] = 1.0
+    w = torch.ones(E, d, device=dev, dtype=torch.bfloat16)
+    L = et.router_logits(x, w)
+    assert bool((L == 2.0 ** 24).all())
+
+
 def test_router_logits_full_size_c3_and_routing(et, orc, dev):
     cfg = W.CONFIGS["C3"]
     T, d, E = cfg["T"], cfg["d"], cfg["E"]
