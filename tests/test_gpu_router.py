@@ -29,6 +29,8 @@ SHAPES = [  # (T, d, E): ragged token tiles, expert counts off the 32-column til
     (300, 256, 200), (129, 64, 256), (64, 7168, 32), (33, 2048, 64), (128, 1024, 96),
     # large batches take the two-token-tile launch shapes (ragged last tile)
     (33001, 136, 40), (66001, 72, 100), (70003, 64, 256), (65536, 520, 128),
+    # the 2 x 2 launch with long rows (4-chunk X ring; 65 chunks, the last one ragged)
+    (33000, 4104, 128),
 ]
 
 
@@ -179,7 +181,7 @@ def _router_case(dev, T, d, E, seed, q):
 ROUTE_SHAPES = [  # (T, d, E, per-expert threshold quantile)
     (1, 8, 1, 0.5), (5, 24, 8, 0.75), (130, 520, 40, 0.9), (1000, 256, 128, 0.95), (300, 256, 200, 0.97),
     (129, 64, 256, 0.99), (33001, 136, 40, 0.8), (66001, 72, 100, 0.93), (70003, 64, 256, 0.97),
-    (16384, 2048, 64, 0.875), (4096, 512, 8, 0.75),
+    (16384, 2048, 64, 0.875), (4096, 512, 8, 0.75), (40000, 4096, 64, 0.875),
 ]
 
 
