@@ -590,6 +590,29 @@ class Step:
                     for j, i in enumerate(stages)}
         return stage_ms, wall_ms
 
+    def graph_ms(self, stages, steps: int) -> float:
+        """Milliseconds per step with the stages captured once in a HIP graph
+        and replayed `steps` times: what a caller that captures the path sees
+        where launches, not bytes, bound the step.  Every stage runs with an
+        explicit slot capacity, so the capture holds no host synchronisation."""
+        import torch
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cs = torch.cuda.current_stream(self.dev)
+            for i in stages:
+                self.stage(i, cs)
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        if int(self.eoff[self.E]) != self.S:
+            raise RuntimeError("routing changed under graph replay")
+        del graph
+        return ms
+
     def sync_outputs(self):
         """Host copies of the routing outputs of the last step."""
         import torch
@@ -667,6 +690,9 @@ def extra_workload(et, lib, dev, workload: str, seed: int, stages, steps: int = 
     stage_ms, wall_ms = st.timed(steps, warmup, stages)
     out = st.summary(stages, stage_ms, wall_ms)
     out["steps"] = steps
+    g_ms = st.graph_ms(stages, steps)
+    out["graph_replay"] = {"ms_per_step": round(g_ms, 4), "slots_per_s": round(st.S / (g_ms * 1e-3), 1),
+                           "hbm_frac": round(out["algorithmic_bytes"] / (g_ms * 1e-3) / HBM_PEAK, 4)}
     if gemm and st.act == torch.bfloat16:
         plan = et.RoutingPlan(st.counts, st.eoff, st.toff, st.st, st.sg, st.ts, st.T, st.E, st.S, st.S)
         out["expert_gemm"] = expert_gemm_brief(et, dev, st.stream, plan, st.X)
@@ -734,24 +760,8 @@ def main() -> int:
                 "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": read_traffic(args.workload),
                 "algorithmic_bytes": abytes[dom], "ms": round(stage_ms[dom], 4)}
 
-    # The same step captured once in a HIP graph and replayed: what a caller
-    # that captures the path sees where launches, not bytes, bound the step
-    # (C1, C5).  Every stage runs with an explicit slot capacity, so the
-    # capture holds no host synchronisation.
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        cs = torch.cuda.current_stream(dev)
-        for i in all_stages:
-            step.stage(i, cs)
-    graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        graph.replay()
-    torch.cuda.synchronize()
-    graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    assert int(step.eoff[E]) == S, "routing changed under graph replay"
-    del graph
+    # The same step captured once in a HIP graph and replayed.
+    graph_ms = step.graph_ms(all_stages, args.steps)
     graph_replay = {"ms_per_step": round(graph_ms, 4), "slots_per_s": round(S / (graph_ms * 1e-3), 1),
                     "hbm_frac": round(step_bytes / (graph_ms * 1e-3) / HBM_PEAK, 4)}
     slots_per_s = S / (ms_per_step * 1e-3)
@@ -819,7 +829,8 @@ def main() -> int:
             x = extras[name]
             print(f"  {name} full size ({'+'.join(x['stages'])}): {x['ms_per_step']:.4f} ms per step, "
                   f"{x['slots_per_s'] / 1e6:.2f} M slots/s, {100 * x['hbm_frac']:.1f}% of HBM peak, mean k "
-                  f"{x['mean_k']}", file=sys.stderr, flush=True)
+                  f"{x['mean_k']}; replayed as a HIP graph {x['graph_replay']['ms_per_step']:.4f} ms "
+                  f"({100 * x['graph_replay']['hbm_frac']:.1f}%)", file=sys.stderr, flush=True)
             if "expert_gemm" in x:
                 b = x["expert_gemm"]
                 print(f"    expert GEMM: gate/up {b['gate_up_ms']:.3f} ms (torch grouped {b['torch_grouped_mm_gate_up_ms']:.3f}"
