@@ -149,10 +149,40 @@ def threshold_dynamics(et, W, dev, stream, workload: str, seed: int) -> dict:
     if not torch.equal(thr, thr_eager):
         raise RuntimeError("graph-replayed threshold dynamics differ from the eager loop")
     del graph
+    # The same loop through et_route_update: the update's selection runs on the
+    # library's second stream beside the routing, the EMA write after both.
+    def combined():
+        for i in range(steps):
+            et.route_update(logits[i], thr, cfg["k_target"], cfg["momentum"], slot_capacity=cap, stat=stat,
+                            workspace=rws, thr_workspace=tws)
+    thr.fill_(cfg["thr0"])
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    combined()
+    b.record(stream)
+    torch.cuda.synchronize()
+    c_ms = a.elapsed_time(b) / steps
+    if not torch.equal(thr, thr_eager):
+        raise RuntimeError("route_update threshold dynamics differ from the eager loop")
+    thr.fill_(cfg["thr0"])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        combined()
+    thr.fill_(cfg["thr0"])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    graph.replay()
+    torch.cuda.synchronize()
+    cg_ms = (time.perf_counter() - t0) * 1e3 / steps
+    if not torch.equal(thr, thr_eager):
+        raise RuntimeError("graph-replayed route_update dynamics differ from the eager loop")
+    del graph
     return {"steps": steps, "T": T, "E": E, "route_ms": round(r_ms / steps, 4),
             "ema_update_ms": round(u_ms / steps, 4), "mean_k_first_step": round(k[0], 4),
             "mean_k_last_step": round(k[-1], 4), "k_target": cfg["k_target"],
-            "graph_replay_ms_per_step": round(g_ms, 4)}
+            "graph_replay_ms_per_step": round(g_ms, 4), "route_update_ms": round(c_ms, 4),
+            "route_update_graph_replay_ms_per_step": round(cg_ms, 4)}
 
 
 def router_producer(et, dev, stream, X, E: int, reps: int = 10) -> dict:
@@ -784,7 +814,9 @@ def main() -> int:
         print(f"  C5 threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
               f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
               f"{dyn['mean_k_last_step']}; all steps replayed as one HIP graph "
-              f"{dyn['graph_replay_ms_per_step']:.4f} ms per step", file=sys.stderr, flush=True)
+              f"{dyn['graph_replay_ms_per_step']:.4f} ms per step; et_route_update (the update beside the "
+              f"routing) {dyn['route_update_ms']:.4f} ms per step, {dyn['route_update_graph_replay_ms_per_step']:.4f} "
+              f"ms replayed", file=sys.stderr, flush=True)
         if step.act == torch.bfloat16 and E <= 256:
             rp = router_producer(et, dev, stream, step.X, E)
             print(f"  router producer: logits {rp['us']:.1f} us ({rp['GB/s']:.0f} GB/s, {100 * rp['frac']:.1f}% of "

@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 9
+#define ET_ABI_VERSION 10
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -214,6 +214,26 @@ size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int64_t num_experts,
                         int64_t k_target, float momentum, float* stat,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Routing and the EMA threshold update of one training batch in one call:
+ * the results of et_route (with the thresholds from before the update)
+ * followed by et_threshold_update, bit for bit.  The update's selection reads
+ * only the logits, so it runs on a second HIP stream of the library's (one per
+ * device, default priority, created on first use) while the routing runs on
+ * `stream`; `stream` then waits for it (HIP events) and applies the EMA.  The
+ * call returns with all work ordered on `stream`, so it can be captured into
+ * a HIP graph.  Workspaces: route_workspace as et_route's, thr_workspace as
+ * et_threshold_update's (two distinct buffers).  Calls from several host
+ * threads are serialised on the side stream.
+ * Composes et_route and et_threshold_update (no reference counterpart).
+ */
+int et_route_update(const float* logits, float* thr, int64_t num_tokens, int64_t num_experts,
+                    int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                    int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
+                    void* route_workspace, size_t route_workspace_bytes,
+                    int64_t k_target, float momentum, float* stat,
+                    void* thr_workspace, size_t thr_workspace_bytes, void* stream);
 
 /* Largest expert count of the router GEMM (all experts of a token tile are
  * accumulated in registers). */

@@ -23,6 +23,7 @@ from .expert_threshold import (  # noqa: F401
     expert_gemm_weight_grad,
     expert_weight_transpose,
     route,
+    route_update,
     route_workspace_bytes,
     router_logits,
     router_route,

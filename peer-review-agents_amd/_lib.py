@@ -54,6 +54,7 @@ _SIGNATURES = {
     "et_dispatch_bwd": (_int, [_p, _p, _p, _i64, _i64, _int, _i64, _p, _p]),
     "et_threshold_workspace_bytes": (_sz, [_i64, _i64]),
     "et_threshold_update": (_int, [_p, _p, _i64, _i64, _i64, _f, _p, _p, _sz, _p]),
+    "et_route_update": (_int, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _sz, _i64, _f, _p, _p, _sz, _p]),
     "et_router_logits": (_int, [_p, _p, _i64, _i64, _i64, _p, _p]),
     "et_router_route_workspace_bytes": (_sz, [_i64, _i64]),
     "et_router_route": (_int, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _sz, _p]),

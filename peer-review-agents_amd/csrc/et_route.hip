@@ -523,7 +523,7 @@ extern "C" size_t et_route_workspace_bytes(int64_t num_tokens, int64_t num_exper
 }
 
 // Argument checks shared by et_route and et_route_noalloc (no HIP call).
-static int route_check(const char* fn, const float* logits, const float* thr, int64_t T, int64_t E,
+int et::route_check(const char* fn, const float* logits, const float* thr, int64_t T, int64_t E,
                        const int32_t* counts, const int32_t* expert_offsets, const int32_t* token_offsets,
                        const int32_t* sorted_token, const float* slot_gate, const int32_t* token_slot,
                        int64_t slot_capacity)

@@ -127,6 +127,13 @@ __device__ __forceinline__ int select_token(const float (&lg)[GM], const float (
 // host-side launchers
 // ---------------------------------------------------------------------------
 
+// Argument checks of et_route (host only; `fn` names the entry point in the
+// error message).  Returns ET_OK or the error code, with et_last_error set.
+int route_check(const char* fn, const float* logits, const float* thr, int64_t T, int64_t E,
+                const int32_t* counts, const int32_t* expert_offsets, const int32_t* token_offsets,
+                const int32_t* sorted_token, const float* slot_gate, const int32_t* token_slot,
+                int64_t slot_capacity);
+
 // Column-wise exclusive scan of the per-block expert counts (NB rows of E)
 // into counts[E] and block_base[NB * E], and of the per-block slot totals
 // into block_slot_base[NB].

@@ -23,8 +23,10 @@
 //     prefix and the rank for the next pass; the last one then histograms the
 //     expert's candidates by their lowest byte and fixes the statistic.
 #include <algorithm>
+#include <mutex>
 
 #include "et_common.hpp"
+#include "et_route_internal.hpp"
 
 namespace et {
 
@@ -292,56 +294,44 @@ __global__ __launch_bounds__(kSelectThreads) void thr_select_kernel(
     uint32_t bin;
     int rin;
     if (find_digit([&](int b) { return hist[b]; }, (int)sel[1], bin, rin)) {
+        // every bit is fixed: p is the statistic (rank 0 marks it found)
         const uint32_t p = p24 | bin;
         prefix[e] = p;
-        rank[e] = (uint32_t)rin;
-        // every bit is fixed: p is the statistic; apply the EMA
-        const float st = u2f(p);
-        if (stat) stat[e] = st;
-        const float one_minus_m = 1.0f - m;
-        thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
+        rank[e] = 0u;
+        if (thr) {
+            const float st = u2f(p);
+            if (stat) stat[e] = st;
+            const float one_minus_m = 1.0f - m;
+            thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
+        }
     }
 }
 
-}  // namespace et
-
-using namespace et;
-
-extern "C" size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts)
+// The EMA of the statistics a stat-only run left in prefix (where rank is 0),
+// with the final select's arithmetic.
+__global__ __launch_bounds__(256) void thr_apply_kernel(int E, const uint32_t* __restrict__ prefix,
+                                                        const uint32_t* __restrict__ rank, float* __restrict__ thr,
+                                                        float* __restrict__ stat, float m)
 {
-    if (num_tokens < 0 || num_experts < 1) return 0;
-    return thr_ws_layout(nullptr, num_tokens, num_experts).bytes;
+    const int e = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (e >= E || rank[e] != 0u) return;
+    const float st = u2f(prefix[e]);
+    if (stat) stat[e] = st;
+    const float one_minus_m = 1.0f - m;
+    thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
 }
 
-extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, int64_t E,
-                                   int64_t k_target, float momentum, float* stat,
-                                   void* workspace, size_t workspace_bytes, void* stream)
+// The radix-select passes on stream s.  With thr, the last select also
+// applies the EMA (and writes stat); without, the statistics stay in
+// ws.prefix for thr_apply_kernel.
+static int thr_passes(const float* logits, int64_t T, int64_t E, int64_t k_target, float* thr, float* stat,
+                      float momentum, const ThrWs& ws, hipStream_t s)
 {
-    if (T < 0) return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: num_tokens < 0");
-    if (E < 1 || E > ET_MAX_EXPERTS)
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: num_experts must be in [1, " +
-                                                 std::to_string(ET_MAX_EXPERTS) + "]");
-    if (T * E >= (int64_t(1) << 31))
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: num_tokens * num_experts must be < 2^31");
-    if (k_target < 1 || k_target > E)
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: k_target must be in [1, num_experts]");
-    if (!(momentum >= 0.0f && momentum <= 1.0f))
-        return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: momentum must be in [0, 1]");
-    if (!thr || !workspace) return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: null thr/workspace");
-    if (T > 0 && !logits) return fail(ET_ERR_INVALID_ARGUMENT, "et_threshold_update: null logits");
-    const ThrWs ws = thr_ws_layout(workspace, T, E);
-    if (workspace_bytes < ws.bytes)
-        return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_threshold_update: workspace needs " +
-                                                    std::to_string(ws.bytes) + " bytes, got " +
-                                                    std::to_string(workspace_bytes));
-    if (T == 0) return ET_OK;
     int64_t c = (T * k_target + E - 1) / E;
     if (c < 1) c = 1;
     if (c > T) c = T;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const int Ti = (int)T, Ei = (int)E;
     const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
-
     for (int pass = 0; pass < 3; ++pass) {
         const int shift = 24 - 8 * pass;
         const HistGrid& g = pass == 0 ? ws.g1 : ws.g2;
@@ -367,4 +357,125 @@ extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, i
         if (int rc = check_launch("thr_select_kernel")) return rc;
     }
     return ET_OK;
+}
+
+// Argument checks of the EMA update (host only).
+static int thr_check(const char* fn, const float* logits, float* thr, int64_t T, int64_t E, int64_t k_target,
+                     float momentum, void* workspace, size_t workspace_bytes)
+{
+    const std::string f(fn);
+    if (T < 0) return fail(ET_ERR_INVALID_ARGUMENT, f + ": num_tokens < 0");
+    if (E < 1 || E > ET_MAX_EXPERTS)
+        return fail(ET_ERR_INVALID_ARGUMENT, f + ": num_experts must be in [1, " + std::to_string(ET_MAX_EXPERTS) + "]");
+    if (T * E >= (int64_t(1) << 31)) return fail(ET_ERR_INVALID_ARGUMENT, f + ": num_tokens * num_experts must be < 2^31");
+    if (k_target < 1 || k_target > E) return fail(ET_ERR_INVALID_ARGUMENT, f + ": k_target must be in [1, num_experts]");
+    if (!(momentum >= 0.0f && momentum <= 1.0f)) return fail(ET_ERR_INVALID_ARGUMENT, f + ": momentum must be in [0, 1]");
+    if (!thr || !workspace) return fail(ET_ERR_INVALID_ARGUMENT, f + ": null thr/workspace");
+    if (T > 0 && !logits) return fail(ET_ERR_INVALID_ARGUMENT, f + ": null logits");
+    const size_t need = thr_ws_layout(nullptr, T, E).bytes;
+    if (workspace_bytes < need)
+        return fail(ET_ERR_WORKSPACE_TOO_SMALL, f + ": workspace needs " + std::to_string(need) + " bytes, got " +
+                                                    std::to_string(workspace_bytes));
+    return ET_OK;
+}
+
+// The library's second stream on each device (default priority), with the
+// two events that fork work onto it and join it back; created on first use.
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kSideDevices = 64;
+static std::mutex g_side_mu;
+static SideStream g_side[kSideDevices];
+
+static int side_stream(const char* fn, SideStream** out)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(ET_ERR_LAUNCH, std::string(fn) + ": hipGetDevice: " + hipGetErrorString(e));
+    if (dev < 0 || dev >= kSideDevices)
+        return fail(ET_ERR_UNSUPPORTED, std::string(fn) + ": device index " + std::to_string(dev) + " beyond " +
+                                            std::to_string(kSideDevices));
+    SideStream& ss = g_side[dev];
+    if (!ss.s) {
+        hipStream_t s = nullptr;
+        hipEvent_t f = nullptr, j = nullptr;
+        e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&f, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&j, hipEventDisableTiming);
+        if (e != hipSuccess)
+            return fail(ET_ERR_LAUNCH, std::string(fn) + ": creating the side stream: " + hipGetErrorString(e));
+        ss.s = s;
+        ss.fork = f;
+        ss.join = j;
+    }
+    *out = &ss;
+    return ET_OK;
+}
+
+}  // namespace et
+
+using namespace et;
+
+extern "C" size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts)
+{
+    if (num_tokens < 0 || num_experts < 1) return 0;
+    return thr_ws_layout(nullptr, num_tokens, num_experts).bytes;
+}
+
+extern "C" int et_threshold_update(const float* logits, float* thr, int64_t T, int64_t E,
+                                   int64_t k_target, float momentum, float* stat,
+                                   void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (int rc = thr_check("et_threshold_update", logits, thr, T, E, k_target, momentum, workspace, workspace_bytes))
+        return rc;
+    if (T == 0) return ET_OK;
+    return thr_passes(logits, T, E, k_target, thr, stat, momentum, thr_ws_layout(workspace, T, E),
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int et_route_update(const float* logits, float* thr, int64_t T, int64_t E, int32_t* counts,
+                               int32_t* expert_offsets, int32_t* token_offsets, int32_t* sorted_token,
+                               float* slot_gate, int32_t* token_slot, int64_t slot_capacity, void* route_workspace,
+                               size_t route_workspace_bytes, int64_t k_target, float momentum, float* stat,
+                               void* thr_workspace, size_t thr_workspace_bytes, void* stream)
+{
+    const char* fn = "et_route_update";
+    if (int rc = route_check(fn, logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
+                             token_slot, slot_capacity))
+        return rc;
+    if (!route_workspace) return fail(ET_ERR_INVALID_ARGUMENT, "et_route_update: null route workspace");
+    if (route_workspace_bytes < et_route_workspace_bytes(T, E))
+        return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_route_update: route workspace needs " +
+                                                    std::to_string(et_route_workspace_bytes(T, E)) + " bytes, got " +
+                                                    std::to_string(route_workspace_bytes));
+    if (int rc = thr_check(fn, logits, thr, T, E, k_target, momentum, thr_workspace, thr_workspace_bytes)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (T == 0)
+        return et_route(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
+                        slot_capacity, route_workspace, route_workspace_bytes, stream);
+    const ThrWs ws = thr_ws_layout(thr_workspace, T, E);
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    SideStream* ss = nullptr;
+    if (int rc = side_stream(fn, &ss)) return rc;
+    // fork: the statistic reads only the logits, so it runs beside the routing
+    hipError_t e = hipEventRecord(ss->fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ss->s, ss->fork, 0);
+    if (e != hipSuccess) return fail(ET_ERR_LAUNCH, std::string("et_route_update: fork: ") + hipGetErrorString(e));
+    const int rc_stat = thr_passes(logits, T, E, k_target, nullptr, nullptr, momentum, ws, ss->s);
+    const int rc_route = rc_stat ? ET_OK
+                                 : et_route(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token,
+                                            slot_gate, token_slot, slot_capacity, route_workspace,
+                                            route_workspace_bytes, stream);
+    // join (also after a failed launch, so the side stream is never left
+    // forked from a capture), then the EMA write, after the routing read thr
+    e = hipEventRecord(ss->join, ss->s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, ss->join, 0);
+    if (e != hipSuccess) return fail(ET_ERR_LAUNCH, std::string("et_route_update: join: ") + hipGetErrorString(e));
+    if (rc_stat) return rc_stat;
+    if (rc_route) return rc_route;
+    thr_apply_kernel<<<dim3((unsigned)((E + 255) / 256)), dim3(256), 0, s>>>((int)E, ws.prefix, ws.rank, thr, stat,
+                                                                             momentum);
+    return check_launch("thr_apply_kernel");
 }

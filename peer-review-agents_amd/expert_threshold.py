@@ -624,6 +624,66 @@ def threshold_update_(thr: torch.Tensor, logits: torch.Tensor, k_target: int,
     return stat
 
 
+def route_update(logits: torch.Tensor, thr: torch.Tensor, k_target: int, momentum: float = 0.99, *,
+                 slot_capacity: Optional[int] = None, stat: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None,
+                 thr_workspace: Optional[torch.Tensor] = None) -> RoutingPlan:
+    """Routing with the current thresholds, then the EMA update of thr from
+    the same batch, in one call: the same results as :func:`route` followed by
+    :func:`threshold_update_`, with the update's selection running on a
+    second HIP stream beside the routing (et_route_update).  It shortens the
+    GPU time of a step replayed from a HIP graph; issued eagerly, its stream
+    fork and join cost more host time than the two calls."""
+    _require(logits, "logits", torch.float32, 2)
+    dev = logits.device
+    T, E = logits.shape
+    _require(thr, "thr", torch.float32, 1, dev)
+    if thr.shape[0] != E:
+        raise ValueError(f"thr has {thr.shape[0]} entries, logits has {E} experts")
+    if not 1 <= E <= ET_MAX_EXPERTS:
+        raise ValueError(f"num_experts must be in [1, {ET_MAX_EXPERTS}], got {E}")
+    if T * E >= 2 ** 31:
+        raise ValueError("num_tokens * num_experts must be < 2^31 (int32 slot indices)")
+    if not 1 <= int(k_target) <= E:
+        raise ValueError(f"k_target must be in [1, {E}], got {k_target}")
+    if not 0.0 <= float(momentum) <= 1.0:
+        raise ValueError(f"momentum must be in [0, 1], got {momentum}")
+    sync = slot_capacity is None
+    cap = T * E if sync else int(slot_capacity)
+    if cap < 0:
+        raise ValueError("slot_capacity must be >= 0")
+    if stat is not None:
+        _out_or_new(stat, (E,), torch.float32, dev, "stat")
+    i32 = dict(dtype=torch.int32, device=dev)
+    counts = torch.empty(E, **i32)
+    eo = torch.empty(E + 1, **i32)
+    to = torch.empty(T + 1, **i32)
+    st = torch.empty(cap, **i32)
+    sg = torch.empty(cap, dtype=torch.float32, device=dev)
+    ts = torch.empty(cap, **i32)
+    rwsb, twsb = route_workspace_bytes(T, E), threshold_workspace_bytes(T, E)
+    if workspace is None:
+        workspace = torch.empty(rwsb, dtype=torch.uint8, device=dev)
+    elif workspace.device != dev or workspace.numel() * workspace.element_size() < rwsb:
+        raise ValueError(f"workspace must hold {rwsb} bytes on {dev}")
+    if thr_workspace is None:
+        thr_workspace = torch.empty(twsb, dtype=torch.uint8, device=dev)
+    elif thr_workspace.device != dev or thr_workspace.numel() * thr_workspace.element_size() < twsb:
+        raise ValueError(f"thr_workspace must hold {twsb} bytes on {dev}")
+    if thr_workspace.data_ptr() == workspace.data_ptr():
+        raise ValueError("workspace and thr_workspace must be distinct buffers")
+    with torch.cuda.device(dev):
+        rc = lib().et_route_update(_vp(logits), _vp(thr), T, E, _vp(counts), _vp(eo), _vp(to), _vp(st), _vp(sg),
+                                   _vp(ts), cap, _vp(workspace), rwsb, int(k_target), float(momentum),
+                                   _vp(stat) if stat is not None else None, _vp(thr_workspace), twsb,
+                                   _stream(dev))
+    check("et_route_update", rc)
+    plan = RoutingPlan(counts, eo, to, st, sg, ts, T, E, cap)
+    if sync:
+        _shrink(plan, int(eo[E].item()))
+    return plan
+
+
 # --------------------------------------------------------------------------- #
 # router producer
 # --------------------------------------------------------------------------- #

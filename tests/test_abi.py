@@ -14,7 +14,7 @@ ET_ERR_WORKSPACE_TOO_SMALL = -2
 
 def test_library_exports_every_header_symbol(et):
     syms = et.header_symbols()
-    assert len(syms) == 25
+    assert len(syms) == 26
     lib = et.lib()
     for name in syms:
         assert hasattr(lib, name), name
@@ -25,8 +25,8 @@ def test_library_exports_every_header_symbol(et):
 
 def test_abi_version_and_header_agree(et):
     hdr = open(os.path.join(ROOT, "include", "etmoe.h")).read()
-    assert "#define ET_ABI_VERSION 9" in hdr
-    assert et.lib().et_abi_version() == 9
+    assert "#define ET_ABI_VERSION 10" in hdr
+    assert et.lib().et_abi_version() == 10
 
 
 def test_workspace_sizes(et):
@@ -108,6 +108,25 @@ def test_threshold_update_rejects_bad_arguments(et):
     assert lib.et_threshold_update(p, p, 16, 8, 2, 0.9, None, p, 8, None) == ET_ERR_WORKSPACE_TOO_SMALL
     # an empty batch is a no-op
     assert lib.et_threshold_update(p, p, 0, 8, 2, 0.9, None, p, 1 << 20, None) == 0
+
+
+def test_route_update_rejects_bad_arguments(et):
+    lib = et.lib()
+    p = ctypes.c_void_p(0x1000)
+    rws = lib.et_route_workspace_bytes(16, 8)
+    tws = lib.et_threshold_workspace_bytes(16, 8)
+
+    def call(T=16, E=8, cap=8, rwsb=rws, k=2, m=0.9, twsb=tws):
+        return lib.et_route_update(p, p, T, E, p, p, p, p, p, p, cap, p, rwsb, k, m, None, p, twsb, None)
+
+    assert call(k=0) == ET_ERR_INVALID_ARGUMENT               # the update's checks
+    assert call(k=9) == ET_ERR_INVALID_ARGUMENT
+    assert call(m=1.5) == ET_ERR_INVALID_ARGUMENT
+    assert call(E=0) == ET_ERR_INVALID_ARGUMENT               # the routing's checks
+    assert call(cap=-1) == ET_ERR_INVALID_ARGUMENT
+    assert call(rwsb=8) == ET_ERR_WORKSPACE_TOO_SMALL
+    assert call(twsb=8) == ET_ERR_WORKSPACE_TOO_SMALL
+    assert "et_route_update" in _err(et)
 
 
 def test_error_string_is_per_call(et):

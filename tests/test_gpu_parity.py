@@ -371,6 +371,75 @@ def test_threshold_update_ties(et, orc, dev, T, E, k):
     np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
 
 
+def _plans_identical(a, b):
+    """Routing outputs equal bit for bit; the slot arrays up to min(S,
+    capacity) (past it they hold whatever the buffer held)."""
+    assert a.num_slots == b.num_slots and a.capacity == b.capacity
+    for f in ("counts", "expert_offsets", "token_offsets"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    n = min(int(a.expert_offsets[-1]), a.capacity)
+    for f in ("sorted_token", "token_slot"):
+        assert torch.equal(getattr(a, f)[:n], getattr(b, f)[:n]), f
+    assert torch.equal(a.slot_gate[:n].view(torch.int32), b.slot_gate[:n].view(torch.int32))
+
+
+@pytest.mark.parametrize("T,E,k,cap", [(8192, 64, 8, None), (1, 4, 2, None), (5000, 128, 8, "under"),
+                                       (131072, 64, 8, "exact"), (300, 1024, 16, None), (999, 7, 3, None)])
+def test_route_update_matches_route_then_update(et, orc, dev, T, E, k, cap):
+    """et_route_update (the update's selection on a second stream) equals
+    route followed by threshold_update_ bit for bit, and the oracle."""
+    print(f"route_update T={T} E={E} k={k} cap={cap}", flush=True)
+    rng = np.random.default_rng([T, E, 5])
+    lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    lg[rng.random((T, E)) < 0.02] = np.nan
+    thr0 = (rng.random(E) * 0.9).astype(np.float32)
+    r = orc.route(lg, thr0)
+    slot_cap = None if cap is None else (r.num_slots // 2 if cap == "under" else r.num_slots)
+    L = dev_f32(lg, dev)
+    thr_a = dev_f32(thr0, dev)
+    plan_a = et.route(L, thr_a, slot_capacity=slot_cap)
+    stat_a = et.threshold_update_(thr_a, L, k, 0.99)
+    thr_b = dev_f32(thr0, dev)
+    stat_b = torch.empty(E, device=dev)
+    plan_b = et.route_update(L, thr_b, k, 0.99, slot_capacity=slot_cap, stat=stat_b)
+    _plans_identical(plan_a, plan_b)
+    np.testing.assert_array_equal(bits(host(thr_b)), bits(host(thr_a)))
+    np.testing.assert_array_equal(bits(host(stat_b)), bits(host(stat_a)))
+    if cap is None:
+        assert_route_equal(plan_b, r)
+    thr_o, stat_o = orc.threshold_update(lg, thr0, k, 0.99)
+    np.testing.assert_array_equal(bits(host(thr_b)), bits(thr_o))
+    np.testing.assert_array_equal(bits(host(stat_b)), bits(stat_o))
+
+
+def test_route_update_graph_replay(et, dev):
+    """et_route_update captured in a HIP graph (its side stream joins the
+    capture): three replays, with eager work and synchronisation between
+    them, each bit-identical to the eager route + update it replaces."""
+    T, E, k, m = 16384, 64, 8, 0.99
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    L = torch.randn(T, E, generator=g, device=dev)
+    cap = T * E
+    warm = torch.full((E,), 0.9, device=dev)
+    et.route_update(L, warm, k, m, slot_capacity=cap)     # creates the library's side stream outside capture
+    torch.cuda.synchronize()
+    thr_g = torch.full((E,), 0.9, device=dev)
+    thr_e = thr_g.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan_g = et.route_update(L, thr_g, k, m, slot_capacity=cap)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        plan_e = et.route(L, thr_e, slot_capacity=cap)
+        et.threshold_update_(thr_e, L, k, m)
+        torch.cuda.synchronize()
+        _plans_identical(plan_g, plan_e)
+        assert torch.equal(thr_g.view(torch.int32), thr_e.view(torch.int32)), rep
+    del graph
+
+
 def test_threshold_dynamics_c5(et, orc, dev):
     """C5 at reduced T: 100 routing steps on fresh logits, EMA after each."""
     cfg = W.CONFIGS["C5"]
