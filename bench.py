@@ -809,65 +809,73 @@ def main() -> int:
     # ---- side measurements (after the timed region) -------------------------------
     dyn = rp = rb = eg = None
     extras = {}
+    extras_error = None
     if not args.no_extras:
-        dyn = threshold_dynamics(et, W, dev, stream, "C5", args.seed)
-        print(f"  C5 threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
-              f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
-              f"{dyn['mean_k_last_step']}; all steps replayed as one HIP graph "
-              f"{dyn['graph_replay_ms_per_step']:.4f} ms per step; et_route_update (the update beside the "
-              f"routing) {dyn['route_update_ms']:.4f} ms per step, {dyn['route_update_graph_replay_ms_per_step']:.4f} "
-              f"ms replayed", file=sys.stderr, flush=True)
-        if step.act == torch.bfloat16 and E <= 256:
-            rp = router_producer(et, dev, stream, step.X, E)
-            print(f"  router producer: logits {rp['us']:.1f} us ({rp['GB/s']:.0f} GB/s, {100 * rp['frac']:.1f}% of "
-                  f"peak; torch bf16 linear {rp['torch_linear_bf16_us']:.1f} us), fused route "
-                  f"{rp['fused_route_us']:.1f} us vs logits + route {rp['logits_then_route_us']:.1f} us",
-                  file=sys.stderr, flush=True)
-        plan_obj = et.RoutingPlan(step.counts, step.eoff, step.toff, step.st, step.sg, step.ts, T, E, S, S)
-        rb = router_backward(et, dev, stream, plan_obj, step.X, step.DXP, step.DGATE, step.DL)
-        print(f"  router backward: dispatch_bwd {rb['dispatch_bwd_us']:.1f} us -> with the router input gradient "
-              f"{rb['dispatch_bwd_router_us']:.1f} us" + (f"; dW {rb['router_wgrad_us']:.1f} us "
-              f"({100 * rb['router_wgrad_frac']:.1f}% of peak; torch f32 mm {rb['torch_mm_f32_wgrad_us']:.1f} us)"
-              if "router_wgrad_us" in rb else ""), file=sys.stderr, flush=True)
-        if step.act == torch.bfloat16 and d % 8 == 0 and S > 0:
-            eg = expert_gemm_leg(et, dev, stream, plan_obj, step.X)
-            gu, dn = eg["gate_up"], eg["down"]
-            print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; with the "
-                  f"SwiGLU epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} "
-                  f"ms + dispatch {gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; "
-                  f"torch grouped {dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
-            g8 = eg["gate_up_fp8"]
-            print(f"  expert GEMM fp8: gate/up {g8['ms']:.3f} ms ({g8['TFLOP/s']:.0f} TFLOP/s, {100 * g8['frac']:.1f}% "
-                  f"of the fp8 peak; with the SwiGLU epilogue {g8['swiglu_epilogue_ms']:.3f} ms; relative error "
-                  f"against bf16 {g8['relative_error_vs_bf16']:.4f}), down {eg['down_fp8']['ms']:.3f} ms "
-                  f"({eg['down_fp8']['TFLOP/s']:.0f} TFLOP/s)", file=sys.stderr)
-            bw = eg["backward"]
-            print(f"  expert GEMM backward: down dA fused with the combine backward "
-                  f"{bw['down_input_grad_fused_combine_bwd_ms']:.3f} ms (transpose {bw['weight_transpose_down_ms']:.3f}),"
-                  f" gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, dW gate/up {bw['gate_up_weight_grad_ms']:.3f} ms "
-                  f"(torch grouped {bw['torch_grouped_mm_gate_up_weight_grad_ms']}), dW down "
-                  f"{bw['down_weight_grad_ms']:.3f} ms", file=sys.stderr)
-            sw = eg["swiglu"]
-            print(f"  SwiGLU for training: forward {sw['forward_ms']:.3f} ms ({100 * sw['forward_frac']:.1f}% of peak), "
-                  f"backward {sw['backward_ms']:.3f} ms ({100 * sw['backward_frac']:.1f}% of peak)", file=sys.stderr,
-                  flush=True)
-        # the other row configurations at full size: C1 (the CPU reference
-        # configuration, f32, all five stages), C2 (variable k, all five
-        # stages) and C4 (one GPU's EP=8 expert share, backward only)
-        for name, stages in (("C1", all_stages), ("C2", all_stages), ("C4", [3, 4])):
-            if name == args.workload or args.no_other_configs:
-                continue
-            extras[name] = extra_workload(et, lib, dev, name, args.seed, stages, gemm=True)
-            x = extras[name]
-            print(f"  {name} full size ({'+'.join(x['stages'])}): {x['ms_per_step']:.4f} ms per step, "
-                  f"{x['slots_per_s'] / 1e6:.2f} M slots/s, {100 * x['hbm_frac']:.1f}% of HBM peak, mean k "
-                  f"{x['mean_k']}; replayed as a HIP graph {x['graph_replay']['ms_per_step']:.4f} ms "
-                  f"({100 * x['graph_replay']['hbm_frac']:.1f}%)", file=sys.stderr, flush=True)
-            if "expert_gemm" in x:
-                b = x["expert_gemm"]
-                print(f"    expert GEMM: gate/up {b['gate_up_ms']:.3f} ms (torch grouped {b['torch_grouped_mm_gate_up_ms']:.3f}"
-                      f" + dispatch {b['dispatch_ms']:.3f}), down {b['down_ms']:.3f} ms (torch grouped "
-                      f"{b['torch_grouped_mm_down_ms']:.3f})", file=sys.stderr, flush=True)
+        # the optional legs: an exception in one is reported in the JSON line
+        # (extras_error) and does not cost the headline measurement
+        try:
+            dyn = threshold_dynamics(et, W, dev, stream, "C5", args.seed)
+            print(f"  C5 threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
+                  f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
+                  f"{dyn['mean_k_last_step']}; all steps replayed as one HIP graph "
+                  f"{dyn['graph_replay_ms_per_step']:.4f} ms per step; et_route_update (the update beside the "
+                  f"routing) {dyn['route_update_ms']:.4f} ms per step, {dyn['route_update_graph_replay_ms_per_step']:.4f} "
+                  f"ms replayed", file=sys.stderr, flush=True)
+            if step.act == torch.bfloat16 and E <= 256:
+                rp = router_producer(et, dev, stream, step.X, E)
+                print(f"  router producer: logits {rp['us']:.1f} us ({rp['GB/s']:.0f} GB/s, {100 * rp['frac']:.1f}% of "
+                      f"peak; torch bf16 linear {rp['torch_linear_bf16_us']:.1f} us), fused route "
+                      f"{rp['fused_route_us']:.1f} us vs logits + route {rp['logits_then_route_us']:.1f} us",
+                      file=sys.stderr, flush=True)
+            plan_obj = et.RoutingPlan(step.counts, step.eoff, step.toff, step.st, step.sg, step.ts, T, E, S, S)
+            rb = router_backward(et, dev, stream, plan_obj, step.X, step.DXP, step.DGATE, step.DL)
+            print(f"  router backward: dispatch_bwd {rb['dispatch_bwd_us']:.1f} us -> with the router input gradient "
+                  f"{rb['dispatch_bwd_router_us']:.1f} us" + (f"; dW {rb['router_wgrad_us']:.1f} us "
+                  f"({100 * rb['router_wgrad_frac']:.1f}% of peak; torch f32 mm {rb['torch_mm_f32_wgrad_us']:.1f} us)"
+                  if "router_wgrad_us" in rb else ""), file=sys.stderr, flush=True)
+            if step.act == torch.bfloat16 and d % 8 == 0 and S > 0:
+                eg = expert_gemm_leg(et, dev, stream, plan_obj, step.X)
+                gu, dn = eg["gate_up"], eg["down"]
+                print(f"  expert GEMM: gate/up {gu['ms']:.3f} ms ({gu['TFLOP/s']:.0f} TFLOP/s, dispatch fused; with the "
+                      f"SwiGLU epilogue {gu['swiglu_epilogue_ms']:.3f} ms; torch grouped {gu['torch_grouped_mm_ms']:.3f} "
+                      f"ms + dispatch {gu['dispatch_ms']:.3f} ms), down {dn['ms']:.3f} ms ({dn['TFLOP/s']:.0f} TFLOP/s; "
+                      f"torch grouped {dn['torch_grouped_mm_ms']:.3f} ms)", file=sys.stderr)
+                g8 = eg["gate_up_fp8"]
+                print(f"  expert GEMM fp8: gate/up {g8['ms']:.3f} ms ({g8['TFLOP/s']:.0f} TFLOP/s, {100 * g8['frac']:.1f}% "
+                      f"of the fp8 peak; with the SwiGLU epilogue {g8['swiglu_epilogue_ms']:.3f} ms; relative error "
+                      f"against bf16 {g8['relative_error_vs_bf16']:.4f}), down {eg['down_fp8']['ms']:.3f} ms "
+                      f"({eg['down_fp8']['TFLOP/s']:.0f} TFLOP/s)", file=sys.stderr)
+                bw = eg["backward"]
+                print(f"  expert GEMM backward: down dA fused with the combine backward "
+                      f"{bw['down_input_grad_fused_combine_bwd_ms']:.3f} ms (transpose {bw['weight_transpose_down_ms']:.3f}),"
+                      f" gate/up dA {bw['gate_up_input_grad_ms']:.3f} ms, dW gate/up {bw['gate_up_weight_grad_ms']:.3f} ms "
+                      f"(torch grouped {bw['torch_grouped_mm_gate_up_weight_grad_ms']}), dW down "
+                      f"{bw['down_weight_grad_ms']:.3f} ms", file=sys.stderr)
+                sw = eg["swiglu"]
+                print(f"  SwiGLU for training: forward {sw['forward_ms']:.3f} ms ({100 * sw['forward_frac']:.1f}% of peak), "
+                      f"backward {sw['backward_ms']:.3f} ms ({100 * sw['backward_frac']:.1f}% of peak)", file=sys.stderr,
+                      flush=True)
+            # the other row configurations at full size: C1 (the CPU reference
+            # configuration, f32, all five stages), C2 (variable k, all five
+            # stages) and C4 (one GPU's EP=8 expert share, backward only)
+            for name, stages in (("C1", all_stages), ("C2", all_stages), ("C4", [3, 4])):
+                if name == args.workload or args.no_other_configs:
+                    continue
+                extras[name] = extra_workload(et, lib, dev, name, args.seed, stages, gemm=True)
+                x = extras[name]
+                print(f"  {name} full size ({'+'.join(x['stages'])}): {x['ms_per_step']:.4f} ms per step, "
+                      f"{x['slots_per_s'] / 1e6:.2f} M slots/s, {100 * x['hbm_frac']:.1f}% of HBM peak, mean k "
+                      f"{x['mean_k']}; replayed as a HIP graph {x['graph_replay']['ms_per_step']:.4f} ms "
+                      f"({100 * x['graph_replay']['hbm_frac']:.1f}%)", file=sys.stderr, flush=True)
+                if "expert_gemm" in x:
+                    b = x["expert_gemm"]
+                    print(f"    expert GEMM: gate/up {b['gate_up_ms']:.3f} ms (torch grouped {b['torch_grouped_mm_gate_up_ms']:.3f}"
+                          f" + dispatch {b['dispatch_ms']:.3f}), down {b['down_ms']:.3f} ms (torch grouped "
+                          f"{b['torch_grouped_mm_down_ms']:.3f})", file=sys.stderr, flush=True)
+        except Exception as exc:  # noqa: BLE001
+            import traceback
+            traceback.print_exc()
+            extras_error = f"{type(exc).__name__}: {exc}"
 
     cpu = None
     if args.cpu_reps > 0:
@@ -900,6 +908,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "copy_ceiling": copy_ref,
         "other_configs": extras or None,
+        "extras_error": extras_error,
         "threshold_dynamics": dyn,
         "router_producer": rp,
         "router_backward": rb,
