@@ -4,21 +4,38 @@
 // X [T, d], on the MFMA units (v_mfma_f32_32x32x16_bf16).
 //
 // The reduction runs over tokens, which is the outer (row) dimension of both
-// operands, so neither loads as MFMA fragments directly (a fragment lane needs
-// 8 consecutive k = tokens).  Each lane therefore loads an 8 x 8 block of X --
-// 8 tokens x 8 consecutive columns, eight 16-byte loads -- and transposes it in
-// registers (v_perm_b32) into 8 B fragments, one per "virtual column tile" j:
-// lane q of tile j is column 8 q + j.  dlogits is loaded 8 tokens per lane
-// (one f32 per load, 128 contiguous bytes per half-wave) and split into
-// hi = bf16(dl) and lo = bf16(dl - hi), two MFMAs each, so dW carries ~16
-// more bits of dl than a bf16 GEMM (exact when dl is a bf16 value).
+// operands, so neither loads as an MFMA fragment directly (a fragment lane
+// needs 8 consecutive k = tokens).  A block stages 64 tokens x 256 columns of
+// X in LDS at a time (row-major, 512-byte rows, a ring of three stages), and
+// each wave forms its X fragments with gfx950's transposing LDS read
+// ds_read_b64_tr_b16: within each 16-lane group, if lane j points at 4
+// consecutive 16-bit elements M[j][0..3], lane i receives M[4 m + i / 4][i % 4]
+// for m = 0..3.  With lane j pointing at row r0 + j / 4, columns c0 + 4 (j % 4),
+// lane i gets column c0 + i of rows r0..r0+3; two such reads give a fragment
+// of 8 consecutive tokens.  Each row stores its 16-byte segment s at slot
+// s ^ (4 (row & 3)), which puts the four rows of one read on distinct 64-byte
+// bank windows.  dlogits is loaded 8 tokens per lane (one f32 per load, 128
+// contiguous bytes per half-wave) and split into hi = bf16(dl) and
+// lo = bf16(dl - hi), two MFMAs each, so dW carries ~16 more bits of dl than
+// a bf16 GEMM (exact when dl is a bf16 value).
 //
-// Work split: a block = one wave per 32-expert tile (up to 4; grid z covers
-// more), all waves on the same 256 columns and token range (the X block is
-// fetched from HBM once and shared through L1/L2).  The token range is split over KS blocks; each
-// writes its partial dW tile, and a second kernel sums the KS partials in
-// order, so the result is deterministic.
+// Schedule: a wave runs one MFMA per slot (32 cycles), and every other
+// instruction of the stage -- the fragment reads and the hi/lo split of the
+// next k-step, the global loads of later stages, the LDS stores of the stage
+// after next -- is placed between two MFMAs, in an order pinned with
+// scheduling barriers, so it issues while the previous MFMA runs instead of in
+// a block of its own.  Stages are separated by a plain s_barrier after the
+// wave's LDS operations are done; loads in flight stay in flight across it.
+//
+// Work split: a block = 4 waves on the same 256 columns and token range.
+// With 3 or more expert tiles (32 experts each) a wave takes one expert tile
+// and all 8 column tiles (grid z covers tiles past 4; a wave whose tile lies
+// past E only stages X); with 2 tiles a wave takes one expert tile and 4
+// column tiles, with 1 tile 2 column tiles.  The token range is split over KS
+// blocks; each writes its partial dW tile, and a second kernel sums the KS
+// partials in order, so the result is deterministic.
 #include <algorithm>
+#include <type_traits>
 
 #include "et_common.hpp"
 
@@ -30,34 +47,47 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 constexpr int kBufDword3 = 0x00020000;           // raw buffer descriptor, word 3 (gfx9)
 constexpr uint32_t kOutOfRange = 0x80000000u;    // offset past every num_records: loads return 0
-constexpr int kColsPerBlock = 256;               // 32 lanes x 8 consecutive columns
-constexpr int kTilesPerBlock = 4;                // expert tiles (waves) per block; grid z covers the rest
+constexpr int kColsPerBlock = 256;               // columns of a block (8 column tiles of 32)
+constexpr int kTilesPerBlock = 4;                // expert tiles per block (one per wave) with 8 column tiles a wave
+constexpr int kThreads = 4 * kWave;
 constexpr int kMaxSplit = 64;
-constexpr int kRing = 2;                         // k-steps of 16 tokens in the load ring
+constexpr int kStageTok = 64;                    // tokens per LDS stage (4 k-steps of 16)
+constexpr int kRowBytes = kColsPerBlock * 2;     // one token's columns in a stage
+constexpr int kStageBytes = kStageTok * kRowBytes;
+constexpr int kStages = 3;                       // LDS ring: stage c in buffer c % 3
+constexpr int kSegs = kStageBytes / 16 / kThreads;   // 16-byte stage segments per thread (8)
+constexpr int kSplitTok = kStageTok;             // a split is a whole number of stages
+constexpr int kMemOps = 8 + 2 * kSegs / 4;       // global loads and LDS stores of a wave per k-step
 
-// The 8 x 8 transpose: xr[i] holds token i's columns 0..7 (2 bf16 per dword);
-// bf[j] gets column j's tokens 0..7.
-__device__ __forceinline__ void transpose8x8(const u32x4_t (&xr)[8], u32x4_t (&bf)[8])
+// LDS byte of 16-byte segment s of stage row r.
+__host__ __device__ constexpr uint32_t stage_off(int r, int s) { return (uint32_t)(r * kRowBytes + ((s ^ (4 * (r & 3))) << 4)); }
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8_t;
+
+__device__ __forceinline__ uint2 read_tr16(const lds_u8_t* p)
 {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            bf[j][k] = __builtin_amdgcn_perm(xr[2 * k + 1][j >> 1], xr[2 * k][j >> 1], sel);
-    }
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+    return __builtin_bit_cast(uint2, v);
 }
 
-// dW partial of one (column block, token range): wave = expert tile n.
-__global__ __launch_bounds__(kTilesPerBlock * kWave) void router_wgrad_kernel(
+// dW partial of one (column block, token range).  NC = column tiles per wave
+// (8, 4 or 2; see the file comment).
+template <int NC>
+__global__ __launch_bounds__(kThreads) void router_wgrad_kernel(
     const float* __restrict__ dl, const uint16_t* __restrict__ x, int T, int d, int E, int tok_per_split,
     int ncb, int nsplit, float* __restrict__ part)
 {
+    __shared__ __attribute__((aligned(16))) unsigned char xs[kStages * kStageBytes];
+    const int tid = threadIdx.x;
     const int lane = lane_id();
-    const int n = (int)blockIdx.z * kTilesPerBlock + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = NC == 8 ? (int)blockIdx.z * kTilesPerBlock + wave : NC == 4 ? (wave & 1) : 0;   // expert tile
+    const int ct0 = NC == 8 ? 0 : NC == 4 ? 4 * (wave >> 1) : 2 * wave;                            // first column tile
     const int q = lane & 31;
     const int h = lane >> 5;
     // XCD-aware block order: consecutive block ids go to the 8 XCDs in turn,
@@ -68,86 +98,199 @@ __global__ __launch_bounds__(kTilesPerBlock * kWave) void router_wgrad_kernel(
     const int xcd = b & 7, slot = b >> 3;
     const int cb = slot % ncb;
     const int ks = xcd + 8 * (slot / ncb);
-    if (ks >= nsplit) return;
-    const int c0 = cb * kColsPerBlock + 8 * q;      // this lane's 8 columns
-    const int e = n * 32 + q;                       // this lane's expert (A rows)
+    if (ks >= nsplit) return;                     // whole block: no barrier is skipped by part of it
+    const int c0 = cb * kColsPerBlock;
+    const int e = n * 32 + q;                     // this lane's expert (A rows)
+    const bool active = n * 32 < E;               // wave-uniform
     const int t_begin = ks * tok_per_split;
     const int t_end = min(T, t_begin + tok_per_split);
+    const int nstage = (t_end - t_begin + kStageTok - 1) / kStageTok;
 
-    const __amdgpu_buffer_rsrc_t xres =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)((int64_t)T * d * 2), kBufDword3);
-    const __amdgpu_buffer_rsrc_t dres =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dl), (short)0, (int)((int64_t)T * E * 4), kBufDword3);
-
-    // loads of one k-step (16 tokens from t): rows t + 8 h + i; rows past the
-    // split or past T, columns past d and experts past E read as 0
-    auto load = [&](int t, u32x4_t (&xr)[8], float (&dv)[8]) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int tt = t + 8 * h + i;
-            const bool ok = tt < t_end;
-            const uint32_t xo = ok && c0 < d ? ((uint32_t)tt * (uint32_t)d + (uint32_t)c0) * 2u : kOutOfRange;
-            const uint32_t dlo = ok && e < E ? ((uint32_t)tt * (uint32_t)E + (uint32_t)e) * 4u : kOutOfRange;
-            xr[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, xo, 0, 0));
-            dv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(dres, dlo, 0, 0));
-        }
+    // Per-stage descriptors start at the stage's first token and end at the
+    // split's end, so rows past it load as 0 by the range check.  Segment i of
+    // this thread is row tid / 32 + 8 i, 16-byte segment tid % 32 (columns
+    // past d: out of range); its LDS slot moves by 8 rows (4096 bytes) per i,
+    // since (row & 3) does not depend on i.  dlogits: lane (q, h), k-step j,
+    // element i is token 16 j + 8 h + i of the stage.
+    const int xcol = c0 + 8 * (tid & 31);
+    const uint32_t xoff0 = xcol < d ? ((uint32_t)(tid >> 5) * (uint32_t)d + (uint32_t)xcol) * 2u : kOutOfRange;
+    const uint32_t xrow8 = (uint32_t)d * 16u;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)xs;
+    const uint32_t xlds0 = lds0 + stage_off(tid >> 5, tid & 31);
+    const uint32_t doff = e < E ? ((uint32_t)(8 * h) * (uint32_t)E + (uint32_t)e) * 4u : kOutOfRange;
+    const uint32_t erow = (uint32_t)E * 4u;
+    // Opaque per-stage copies of the lane offsets: the offsets of the
+    // individual loads are formed next to each load instead of being kept
+    // live across the loop (32 + 8 registers).
+    uint32_t xo = xoff0, dof = doff;
+    auto refresh = [&]() {
+        xo = xoff0;
+        dof = doff;
+        asm volatile("" : "+v"(xo), "+v"(dof));
     };
-
-    f32x16_t acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = f32x16_t{};
-
-    auto compute = [&](const u32x4_t (&xr)[8], const float (&dv)[8]) {
-        u32x4_t bf[8];
-        transpose8x8(xr, bf);
-        u32x4_t ahi, alo;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            ahi[k] = pack_bf16x2(dv[2 * k], dv[2 * k + 1]);
-            const float r0 = dv[2 * k] - bf16lo(ahi[k]);
-            const float r1 = dv[2 * k + 1] - bf16hi(ahi[k]);
-            alo[k] = pack_bf16x2(r0, r1);
-        }
-        const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, ahi), al = __builtin_bit_cast(bf16x8_t, alo);
-        // all hi terms, then all lo terms: the two MFMAs on one accumulator are
-        // 8 apart, so none waits for the previous one's result
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, __builtin_bit_cast(bf16x8_t, bf[j]), acc[j], 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, __builtin_bit_cast(bf16x8_t, bf[j]), acc[j], 0, 0, 0);
+    // (read as wave-uniform explicitly: the clamp is formed on the vector unit,
+    // and a descriptor field in a vector register costs a loop per load)
+    auto nrow_of = [&](int c) {
+        return __builtin_amdgcn_readfirstlane(max(0, min(kStageTok, t_end - (t_begin + c * kStageTok))));
     };
-
-    // A ring of kRing k-steps: the loads of step s + kRing - 1 are issued
-    // before step s is computed.  The loop runs whole groups of kRing steps
-    // over the split (its length is a multiple of 16 kRing tokens) with no
-    // exit inside, so the accumulators and the ring keep their registers;
-    // steps past t_end load zeros and add nothing.
-    u32x4_t xr[kRing][8];
-    float dv[kRing][8];
+    // X fragment of column tile ct0 + cc: lane group gq = lane / 16 reads
+    // column 32 (ct0 + cc) + 16 (gq & 1) + lane % 16 of rows
+    // 16 j + 8 (gq >> 1) + 0..7 of the k-step.
+    const int gq = lane >> 4, i16 = lane & 15;
+    const int rrow = 8 * (gq >> 1) + (i16 >> 2);
+    uint32_t rb[NC];
 #pragma unroll
-    for (int p = 0; p < kRing - 1; ++p) load(t_begin + 16 * p, xr[p], dv[p]);
-    for (int t = t_begin; t < t_end; t += 16 * kRing) {
-#pragma unroll
-        for (int r = 0; r < kRing; ++r) {
-            __builtin_amdgcn_sched_barrier(0);
-            load(t + 16 * (r + kRing - 1), xr[(r + kRing - 1) % kRing], dv[(r + kRing - 1) % kRing]);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(xr[r], dv[r]);
-        }
+    for (int cc = 0; cc < NC; ++cc) {
+        const int col = 32 * (ct0 + cc) + 16 * (gq & 1) + 4 * (i16 & 3);
+        rb[cc] = stage_off(rrow, col >> 3) + (col & 7) * 2;
     }
 
-    // partial tile: lane (q, h) holds columns c0 .. c0 + 7 (acc[0..7]) of
-    // expert rows n * 32 + 8 (r / 4) + 4 h + r % 4
+    f32x16_t acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) acc[j] = f32x16_t{};
+    u32x4_t xr[kSegs];        // X of stage c + 2 (to LDS in stage c), then of stage c + 3
+    float dv[4][8];           // dlogits of k-step j: stage c until converted (during k-step j - 1), then stage c + 1
+    u32x4_t af[2][2];         // A fragments (hi, lo) of k-steps j (af[j & 1]) and j + 1
+    u32x4_t bf[2][NC];        // X fragments of k-steps j and j + 1
+
+    auto load_x = [&](int c, u32x4_t (&dst)[kSegs], int i) {
+        const __amdgpu_buffer_rsrc_t res = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(x + (int64_t)(t_begin + c * kStageTok) * d), (short)0, nrow_of(c) * d * 2, kBufDword3);
+        dst[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(res, xo + (uint32_t)i * xrow8, 0, 0));
+    };
+    auto store_x = [&](int c, const u32x4_t (&src)[kSegs], int i) {
+        const uint32_t a = xlds0 + (uint32_t)(c % kStages) * kStageBytes + 4096u * i;
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>((uintptr_t)a) = src[i];
+    };
+    auto load_dl = [&](int c, int j, int i) {
+        const __amdgpu_buffer_rsrc_t res = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(dl + (int64_t)(t_begin + c * kStageTok) * E), (short)0, nrow_of(c) * E * 4, kBufDword3);
+        dv[j][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, dof + (uint32_t)(16 * j + i) * erow, 0, 0));
+    };
+    // hi/lo split of elements 2 k, 2 k + 1 of a k-step's dlogits
+    auto convert = [&](const float (&v)[8], u32x4_t (&a)[2], int k) {
+        const uint32_t hw = pack_bf16x2(v[2 * k], v[2 * k + 1]);
+        a[0][k] = hw;
+        a[1][k] = pack_bf16x2(v[2 * k] - bf16lo(hw), v[2 * k + 1] - bf16hi(hw));
+    };
+    // Fragment bases of column tile cc in the buffers of stages c and c + 1,
+    // formed once a stage; k-step and half are immediate offsets.
+    const lds_u8_t* rp[2][NC];
+    auto set_bases = [&](int c) {
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+            uint32_t a0 = lds0 + (uint32_t)(c % kStages) * kStageBytes + rb[cc];
+            uint32_t a1 = lds0 + (uint32_t)((c + 1) % kStages) * kStageBytes + rb[cc];
+            // opaque: keeps the k-step and half offsets in the instructions'
+            // offset fields instead of 32 precomputed addresses per stage
+            asm volatile("" : "+v"(a0), "+v"(a1));
+            rp[0][cc] = (const lds_u8_t*)(uintptr_t)a0;
+            rp[1][cc] = (const lds_u8_t*)(uintptr_t)a1;
+        }
+    };
+    // half hf (rows +0 or +4) of the fragment of column tile cc, k-step j of
+    // stage c + nx
+    auto read_half = [&](int nx, int j, int cc, int hf, u32x4_t& dst) {
+        const uint2 v = read_tr16(rp[nx][cc] + 8192 * j + 2048 * hf);
+        if (hf == 0) {
+            dst[0] = v.x;
+            dst[1] = v.y;
+        } else {
+            dst[2] = v.x;
+            dst[3] = v.y;
+        }
+    };
+    auto pin = [&]() { __builtin_amdgcn_sched_barrier(0); };
+    auto barrier = [&]() {
+        pin();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        pin();
+    };
+    // memory op m of k-step j of stage c (m < kMemOps): segments 2 j, 2 j + 1
+    // of the X of stage c + 2 to its LDS buffer (last read in stage c - 1,
+    // before the previous barrier), the same segments of the X of stage c + 3
+    // into their registers, then the dlogits of k-step j of stage c + 1 (this
+    // k-step's own were split during k-step j - 1)
+    auto mem_op = [&](int c, int j, int m, auto act) {
+        if (m < 2) store_x(c + 2, xr, 2 * j + m);
+        else if (m < 4) load_x(c + 3, xr, 2 * j + m - 2);
+        else if (decltype(act)::value) load_dl(c + 1, j, m - 4);
+    };
+
+    auto run = [&](auto act) {
+        constexpr bool A = decltype(act)::value;
+        refresh();
+#pragma unroll
+        for (int i = 0; i < kSegs; ++i) load_x(0, xr, i);
+#pragma unroll
+        for (int i = 0; i < kSegs; ++i) store_x(0, xr, i);
+#pragma unroll
+        for (int i = 0; i < kSegs; ++i) load_x(1, xr, i);
+#pragma unroll
+        for (int i = 0; i < kSegs; ++i) store_x(1, xr, i);
+#pragma unroll
+        for (int i = 0; i < kSegs; ++i) load_x(2, xr, i);
+        if (A) {
+#pragma unroll
+            for (int m = 0; m < 32; ++m) load_dl(0, m >> 3, m & 7);
+        }
+        barrier();
+        if (A) {
+            set_bases(0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) convert(dv[0], af[0], k);
+#pragma unroll
+            for (int u = 0; u < 2 * NC; ++u) read_half(0, 0, u >> 1, u & 1, bf[0][u >> 1]);
+        }
+        // stage c, c & 1 == par: 4 k-steps x 2 NC slots
+        auto stage = [&](int c, auto parc) {
+            constexpr int par = decltype(parc)::value;
+            constexpr int S = 8 * NC;
+            refresh();
+            if (A) set_bases(c);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int j = s / (2 * NC), u = s % (2 * NC);
+                if (A) {
+                    const int cc = u % NC;
+                    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, af[j & 1][u < NC ? 0 : 1]);
+                    acc[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8_t, bf[j & 1][cc]),
+                                                                      acc[cc], 0, 0, 0);
+                    pin();
+                    // next k-step: j + 1 of this stage, or k-step 0 of stage c + 1
+                    read_half(j == 3 ? 1 : 0, (j + 1) & 3, u >> 1, u & 1, bf[(j + 1) & 1][u >> 1]);
+                    if (u % (NC / 2) == 0 && u / (NC / 2) < 4)
+                        convert(dv[(j + 1) & 3], af[(j + 1) & 1], u / (NC / 2));
+                }
+                // memory ops m of this k-step with m * 2 NC / kMemOps == u
+#pragma unroll
+                for (int m = (u * kMemOps + 2 * NC - 1) / (2 * NC); m < ((u + 1) * kMemOps + 2 * NC - 1) / (2 * NC); ++m)
+                    mem_op(c, j, m, act);
+                pin();
+            }
+            barrier();
+        };
+        for (int c = 0; c < nstage; c += 2) {
+            stage(c, std::integral_constant<int, 0>{});
+            if (c + 1 < nstage) stage(c + 1, std::integral_constant<int, 1>{});
+        }
+    };
+    if (active) run(std::true_type{});
+    else run(std::false_type{});
+
+    // partial tile: lane (q, h) holds column c0 + 32 (ct0 + cc) + q (acc[cc])
+    // of expert rows n * 32 + 8 (r / 4) + 4 h + r % 4
+    if (!active) return;
     float* pt = part + (int64_t)ks * E * d;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = n * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-        if (row < E && c0 < d) {
-            float* dst = pt + (int64_t)row * d + c0;
-            *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-            *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+        if (row < E) {
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) {
+                const int col = c0 + 32 * (ct0 + cc) + q;
+                if (col < d) pt[(int64_t)row * d + col] = acc[cc][r];
+            }
         }
     }
 }
@@ -177,21 +320,23 @@ __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float* _
 }
 
 struct WgradPlan {
-    int ncb, nt, ks, tok_per_split;
+    int ncb, nt, nz, nc, ks, tok_per_split;
 };
 
-// Splits the tokens so that the grid holds about 1024 waves (one per SIMD):
-// columns blocks x expert tiles x splits.
+// Column tiles per wave (8 from 3 expert tiles up), and splits of the tokens
+// so that the grid holds about 256 blocks of 4 waves (one wave per SIMD).
 WgradPlan wgrad_plan(int64_t T, int64_t d, int64_t E)
 {
     WgradPlan p;
     p.ncb = (int)((d + kColsPerBlock - 1) / kColsPerBlock);
     p.nt = (int)((E + 31) / 32);
-    const int64_t want = (1024 + (int64_t)p.ncb * p.nt - 1) / ((int64_t)p.ncb * p.nt);
-    const int64_t max_by_t = std::max<int64_t>(1, (T + 63) / 64);
+    p.nc = p.nt >= 3 ? 8 : p.nt == 2 ? 4 : 2;
+    p.nz = p.nc == 8 ? (p.nt + kTilesPerBlock - 1) / kTilesPerBlock : 1;
+    const int64_t want = (256 + (int64_t)p.ncb * p.nz - 1) / ((int64_t)p.ncb * p.nz);
+    const int64_t max_by_t = std::max<int64_t>(1, (T + kSplitTok - 1) / kSplitTok);
     p.ks = (int)std::max<int64_t>(1, std::min<int64_t>({want, (int64_t)kMaxSplit, max_by_t}));
     const int64_t per = (T + p.ks - 1) / p.ks;
-    p.tok_per_split = (int)(((per + 16 * kRing - 1) / (16 * kRing)) * (16 * kRing));
+    p.tok_per_split = (int)(((per + kSplitTok - 1) / kSplitTok) * kSplitTok);
     p.ks = (int)std::max<int64_t>(1, (T + p.tok_per_split - 1) / p.tok_per_split);
     return p;
 }
@@ -238,10 +383,18 @@ extern "C" int et_router_wgrad(const float* dlogits, const void* x, int64_t T, i
         return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_router_wgrad: workspace needs " + std::to_string(need) +
                                                     " bytes, got " + std::to_string(workspace_bytes));
     float* part = static_cast<float*>(workspace);
-    const int nz = (p.nt + kTilesPerBlock - 1) / kTilesPerBlock;
     const unsigned nblk = (unsigned)(p.ncb * ((p.ks + 7) / 8) * 8);   // split groups of 8 (one per XCD)
-    router_wgrad_kernel<<<dim3(nblk, 1, nz), dim3(std::min(p.nt, kTilesPerBlock) * kWave), 0, s>>>(
-        dlogits, static_cast<const uint16_t*>(x), (int)T, (int)d, (int)E, p.tok_per_split, p.ncb, p.ks, part);
+    const dim3 grid(nblk, 1, (unsigned)p.nz);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    if (p.nc == 8)
+        router_wgrad_kernel<8><<<grid, dim3(kThreads), 0, s>>>(dlogits, xb, (int)T, (int)d, (int)E, p.tok_per_split,
+                                                                p.ncb, p.ks, part);
+    else if (p.nc == 4)
+        router_wgrad_kernel<4><<<grid, dim3(kThreads), 0, s>>>(dlogits, xb, (int)T, (int)d, (int)E, p.tok_per_split,
+                                                                p.ncb, p.ks, part);
+    else
+        router_wgrad_kernel<2><<<grid, dim3(kThreads), 0, s>>>(dlogits, xb, (int)T, (int)d, (int)E, p.tok_per_split,
+                                                                p.ncb, p.ks, part);
     if (int rc = check_launch("router_wgrad_kernel")) return rc;
     router_wgrad_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(part, p.ks, n4, dw);
     return check_launch("router_wgrad_reduce_kernel");

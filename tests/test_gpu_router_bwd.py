@@ -134,7 +134,7 @@ def test_dispatch_bwd_router_composes_with_combine_backward(et, dev):
 
 WGRAD_SHAPES = [  # (T, d, E): ragged token splits, E off the 32-wide tile, d off the 256-column block
     (1, 8, 1), (100, 264, 40), (4097, 1024, 128), (33001, 136, 100), (7000, 72, 256), (65536, 512, 128),
-    (333, 4096, 8),
+    (333, 4096, 8), (2000, 1040, 64), (5000, 776, 96), (129, 264, 33),
 ]
 
 
