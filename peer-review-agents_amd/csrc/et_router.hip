@@ -54,10 +54,16 @@ template <> struct RtMfma<16> {
     static constexpr int KS = 32;
     static constexpr int NACC = 4;
     typedef f32x4_t Acc;
+    // Both forms are written as inline assembly with the accumulator tied in
+    // place ("+a"): with the builtin, the register allocator gave some
+    // products a new accumulator register and restored them with ~160
+    // accumulator moves per chunk (over 1000 per tile at 8 expert tiles).  The
+    // compiler does not see these as MFMAs, so the kernel waits out their
+    // latency itself before it reads the accumulators.
     static __device__ __forceinline__ Acc mma(u32x4_t a, u32x4_t b, Acc c)
     {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                       c, 0, 0, 0);
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        return c;
     }
     static __device__ __forceinline__ int crow(int lane, int j) { return 4 * (lane >> 4) + j; }
     // 16-token route group (within the wave) of element j of token tile m
@@ -69,8 +75,8 @@ template <> struct RtMfma<32> {
     typedef f32x16_t Acc;
     static __device__ __forceinline__ Acc mma(u32x4_t a, u32x4_t b, Acc c)
     {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                       c, 0, 0, 0);
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        return c;
     }
     static __device__ __forceinline__ int crow(int lane, int j) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
     static constexpr int group(int m, int j) { return 2 * m + j / 8; }
@@ -325,15 +331,16 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             kBufDword3);
 
         u32x4_t wreg[2][S::SEGS_PER_THREAD];
+        auto load_w_one = [&](int c, u32x4_t (&wr)[S::SEGS_PER_THREAD], int i) {
+            const int seg = min(tid + i * S::THREADS, S::SEGS - 1);
+            const int e = seg / (S::KC / 8);
+            const int k = chunk_at(c) * S::KC + (seg % (S::KC / 8)) * 8;
+            const uint32_t off = k < d ? ((uint32_t)e * (uint32_t)d + (uint32_t)k) * 2u : kBufOutOfRange;
+            wr[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wres, off, 0, 0));
+        };
         auto load_w = [&](int c, u32x4_t (&wr)[S::SEGS_PER_THREAD]) {
 #pragma unroll
-            for (int i = 0; i < S::SEGS_PER_THREAD; ++i) {
-                const int seg = min(tid + i * S::THREADS, S::SEGS - 1);
-                const int e = seg / (S::KC / 8);
-                const int k = chunk_at(c) * S::KC + (seg % (S::KC / 8)) * 8;
-                const uint32_t off = k < d ? ((uint32_t)e * (uint32_t)d + (uint32_t)k) * 2u : kBufOutOfRange;
-                wr[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wres, off, 0, 0));
-            }
+            for (int i = 0; i < S::SEGS_PER_THREAD; ++i) load_w_one(c, wr, i);
         };
         auto store_w = [&](int buf, const u32x4_t (&wr)[S::SEGS_PER_THREAD]) {
 #pragma unroll
@@ -347,16 +354,26 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             }
         };
         u32x4_t xr[R][S::TT][S::KSTEPS];
+        auto load_x_one = [&](int c, u32x4_t (&a)[S::TT][S::KSTEPS], int m, int s) {
+            const int k = chunk_at(c) * S::KC + s * F::KS + quad * 8;
+            const uint32_t off = k < d ? (uint32_t)(m * M + row) * (uint32_t)d * 2u + (uint32_t)k * 2u : kBufOutOfRange;
+            a[m][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
+        };
         auto load_x = [&](int c, u32x4_t (&a)[S::TT][S::KSTEPS]) {
 #pragma unroll
             for (int m = 0; m < S::TT; ++m)
 #pragma unroll
-                for (int s = 0; s < S::KSTEPS; ++s) {
-                    const int k = chunk_at(c) * S::KC + s * F::KS + quad * 8;
-                    const uint32_t off =
-                        k < d ? (uint32_t)(m * M + row) * (uint32_t)d * 2u + (uint32_t)k * 2u : kBufOutOfRange;
-                    a[m][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
-                }
+                for (int s = 0; s < S::KSTEPS; ++s) load_x_one(c, a, m, s);
+        };
+        // load i of a step (W chunk segments first, then X chunk rows), so the
+        // loads can be spread between the step's MFMAs in issue order
+        constexpr int NLOADS = S::SEGS_PER_THREAD + S::TT * S::KSTEPS;
+        auto load_one = [&](int c, int r, int i) {
+            if (i < S::SEGS_PER_THREAD) load_w_one(c + 2, wreg[r & 1], i);
+            else {
+                const int j = i - S::SEGS_PER_THREAD;
+                load_x_one(c + S::PF, xr[(r + S::PF) % R], j / S::KSTEPS, j % S::KSTEPS);
+            }
         };
 
         typename F::Acc acc[S::TT][S::ET];
@@ -380,11 +397,17 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             // Loads complete in issue order and the scheduler must not reorder
             // these: the wait for W chunk c + 1 at the end of the step then
             // leaves X chunks c + 2 .. c + R - 1 in flight.
+            // With the 16 x 16 form the loads go one after each of the
+            // step's first MFMAs (issued while the MFMA runs); with the 32 x
+            // 32 form they stay a block ahead of the MFMAs.
+            constexpr bool SPREAD = M == 16;
             __builtin_amdgcn_sched_barrier(0);
-            load_w(c + 2, wreg[r & 1]);
-            __builtin_amdgcn_sched_barrier(0);
-            load_x(c + S::PF, xr[(r + S::PF) % R]);
-            __builtin_amdgcn_sched_barrier(0);
+            if (!SPREAD) {
+                load_w(c + 2, wreg[r & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                load_x(c + S::PF, xr[(r + S::PF) % R]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             constexpr int UT = S::ET / S::UPS;       // expert tiles per unit
             constexpr int NU = S::UPS * S::KSTEPS;
             const uint16_t* wb = wl[r & 1];
@@ -405,8 +428,15 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
 #pragma unroll
                 for (int n = 0; n < UT; ++n)
 #pragma unroll
-                    for (int m = 0; m < S::TT; ++m)
+                    for (int m = 0; m < S::TT; ++m) {
                         acc[m][n0 + n] = F::mma(xr[r][m][s], bf[u & 1][n], acc[m][n0 + n]);
+                        const int g = (u * UT + n) * S::TT + m;      // MFMA index within the step
+                        if (SPREAD && g < NLOADS) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            load_one(c, r, g);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
                 __builtin_amdgcn_sched_barrier(0);
             }
             store_w((r + 1) & 1, wreg[(r + 1) & 1]);
@@ -424,6 +454,9 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
         for (int r = 0; r < R - 1; ++r)
             if (nmain + r < nchunks) step(nmain + r, r);
 
+        // wait until the last products are written (at most 16 passes of 4
+        // cycles after issue; 80 cycles of s_nop)
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
         // epilogue: lane l writes expert n * M + l % M of its token rows per tile
         if (!ROUTE || logits != nullptr) {
 #pragma unroll
