@@ -43,7 +43,10 @@
  *    dlogits is 0 at dropped pairs, and the rows of dropped slots below the
  *    capacity are left as they were (their dgate is 0 or left as it was).
  *  - Concurrent calls on different streams are safe when their buffers are
- *    disjoint (the library keeps no device state).
+ *    disjoint.  Two entry points hold device state: et_route_noalloc's static
+ *    scratch (one per GPU, shared by its calls) and et_route_update's side
+ *    stream (one per GPU, used only under HIP graph capture, serialised by a
+ *    mutex); every other entry point keeps none.
  */
 #ifndef ETMOE_H
 #define ETMOE_H
@@ -55,7 +58,7 @@
 extern "C" {
 #endif
 
-#define ET_ABI_VERSION 10
+#define ET_ABI_VERSION 11
 
 /* activation dtypes */
 #define ET_DTYPE_F32 0
@@ -76,7 +79,9 @@ int et_abi_version(void);
 /* Message of the last failed call on this host thread ("" if none). */
 const char* et_last_error(void);
 
-/* Bytes of device workspace et_route needs for T tokens and E experts. */
+/* Bytes of device workspace et_route needs for T tokens and E experts: the
+ * routed pairs of every 8-token group (8 * E entries of 8 bytes reserved per
+ * group, about 8 * T * E bytes in all) plus per-group and per-tile counts. */
 size_t et_route_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 
 /*
@@ -112,9 +117,11 @@ int et_route(const float* logits, const float* thr, int64_t num_tokens, int64_t 
  * et_route (bit-identical results); the call runs on the current device, whose
  * scratch address it looks up once (on its first call there).  Sizes whose
  * et_route_workspace_bytes(T, E) exceeds the scratch are rejected with
- * ET_ERR_WORKSPACE_TOO_SMALL: every T fits for E <= 408 (the workspace depends
- * on E and only weakly on T).  All calls on one GPU share the scratch: calls
- * that overlap in time on one GPU (different streams or host threads) race.
+ * ET_ERR_WORKSPACE_TOO_SMALL: every T fits for E <= 408.  It runs the two-read
+ * routing kernels (a count pass and a fill pass that both read the logits),
+ * whose workspace is O(E) per block, not et_route's pair lists.  All calls on
+ * one GPU share the scratch: calls that overlap in time on one GPU (different
+ * streams or host threads) race.
  * No counterpart in the reference: an extra entry point of this library.
  */
 int et_route_noalloc(const float* logits, const float* thr, int64_t num_tokens, int64_t num_experts,
@@ -143,10 +150,10 @@ int et_combine_fwd(const void* yp, const float* slot_gate, const int32_t* token_
                    int64_t slot_capacity, void* y, void* stream);
 
 /* Bytes of device workspace et_combine_bwd needs when a row is a whole number
- * of 16-byte chunks (else 0): slot_capacity * ceil(d * elem / 1024) doubles of
- * partial dot products, then, from the next 256-byte boundary, the slot walk
- * order (slot_capacity int32).  num_tokens does not enter.  The workspace must
- * be 8-byte aligned. */
+ * of 16-byte chunks (else 0): slot_capacity * ceil(ceil(d * elem / 1024) / 2)
+ * doubles of partial dot products (one per 2 KiB of the row), then, from the
+ * next 256-byte boundary, the slot walk order (slot_capacity int32).
+ * num_tokens does not enter.  The workspace must be 8-byte aligned. */
 size_t et_combine_bwd_workspace_bytes(int64_t num_tokens, int64_t slot_capacity, int64_t d, int dtype);
 
 /*
@@ -198,8 +205,8 @@ int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, const 
                            size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace et_threshold_update needs for T tokens and E experts
- * (it holds the T*E score keys, T*E candidate keys for the last digit and the
- * radix-select histograms: about 8*T*E bytes). */
+ * (it holds the top 16 bits of the T*E score keys, up to T*E candidate keys
+ * for the last 14 bits and the radix-select histograms: about 6*T*E bytes). */
 size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 
 /*
@@ -218,14 +225,18 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
 /*
  * Routing and the EMA threshold update of one training batch in one call:
  * the results of et_route (with the thresholds from before the update)
- * followed by et_threshold_update, bit for bit.  The update's selection reads
- * only the logits, so it runs on a second HIP stream of the library's (one per
- * device, default priority, created on first use) while the routing runs on
- * `stream`; `stream` then waits for it (HIP events) and applies the EMA.  The
- * call returns with all work ordered on `stream`, so it can be captured into
- * a HIP graph.  Workspaces: route_workspace as et_route's, thr_workspace as
- * et_threshold_update's (two distinct buffers).  Calls from several host
- * threads are serialised on the side stream.
+ * followed by et_threshold_update, bit for bit.  Issued eagerly it enqueues
+ * exactly those two calls' kernels on `stream`.  While `stream` is being
+ * captured into a HIP graph, the update's selection (which reads only the
+ * logits) goes on a second HIP stream of the library's (one per device,
+ * default priority, created on the first such call), a parallel branch beside
+ * the routing; `stream` then joins it (HIP events) and applies the EMA, so
+ * the captured work still ends on `stream`.  If that side stream already
+ * belongs to another capture (another host thread, or an earlier call of the
+ * same capture), the call falls back to the single-stream order.
+ * Workspaces: route_workspace as et_route's, thr_workspace as
+ * et_threshold_update's; their byte ranges must not overlap
+ * (ET_ERR_INVALID_ARGUMENT).
  * Composes et_route and et_threshold_update (no reference counterpart).
  */
 int et_route_update(const float* logits, float* thr, int64_t num_tokens, int64_t num_experts,

@@ -45,6 +45,8 @@ __device__ __forceinline__ void load_thresholds(const float* __restrict__ thr, i
 // strictly between the bounds, and NaN logits, need the exact score.
 //   th NaN or > 1: nothing is selected (hi = NaN, lo = +inf).
 //   th <= 0:       every non-NaN logit is selected (hi = -inf, lo = NaN).
+// The searches stay loops (not unrolled): the bounds are computed once per
+// wave or block, and 48 inlined sigmoids would crowd the instruction cache.
 __device__ __forceinline__ void select_bounds(float th, float& hi, float& lo)
 {
     const float inf = __builtin_huge_valf();
@@ -56,6 +58,7 @@ __device__ __forceinline__ void select_bounds(float th, float& hi, float& lo)
     const float s0 = __builtin_fmaxf(__builtin_fabsf(l0) * 0x1p-18f, 0x1p-20f);
     hi = nan;
     float step = s0;
+#pragma unroll 1
     for (int it = 0; it < 24; ++it) {
         const float h = l0 + step;
         if (f2u(sigmoid(h)) >= tb + 2u) { hi = h; break; }
@@ -63,6 +66,7 @@ __device__ __forceinline__ void select_bounds(float th, float& hi, float& lo)
     }
     lo = nan;
     step = s0;
+#pragma unroll 1
     for (int it = 0; it < 24; ++it) {
         const float g = l0 - step;
         if (f2u(sigmoid(g)) + 2u < tb) { lo = g; break; }

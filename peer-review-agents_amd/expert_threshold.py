@@ -630,10 +630,10 @@ def route_update(logits: torch.Tensor, thr: torch.Tensor, k_target: int, momentu
                  thr_workspace: Optional[torch.Tensor] = None) -> RoutingPlan:
     """Routing with the current thresholds, then the EMA update of thr from
     the same batch, in one call: the same results as :func:`route` followed by
-    :func:`threshold_update_`, with the update's selection running on a
-    second HIP stream beside the routing (et_route_update).  It shortens the
-    GPU time of a step replayed from a HIP graph; issued eagerly, its stream
-    fork and join cost more host time than the two calls."""
+    :func:`threshold_update_` (et_route_update).  Issued eagerly it enqueues
+    exactly those two calls' kernels on the current stream; captured into a
+    HIP graph, the update's selection becomes a parallel branch beside the
+    routing, which shortens the replayed step."""
     _require(logits, "logits", torch.float32, 2)
     dev = logits.device
     T, E = logits.shape
@@ -670,8 +670,9 @@ def route_update(logits: torch.Tensor, thr: torch.Tensor, k_target: int, momentu
         thr_workspace = torch.empty(twsb, dtype=torch.uint8, device=dev)
     elif thr_workspace.device != dev or thr_workspace.numel() * thr_workspace.element_size() < twsb:
         raise ValueError(f"thr_workspace must hold {twsb} bytes on {dev}")
-    if thr_workspace.data_ptr() == workspace.data_ptr():
-        raise ValueError("workspace and thr_workspace must be distinct buffers")
+    a, b = workspace.data_ptr(), thr_workspace.data_ptr()
+    if a < b + twsb and b < a + rwsb:
+        raise ValueError("workspace and thr_workspace must not overlap")
     with torch.cuda.device(dev):
         rc = lib().et_route_update(_vp(logits), _vp(thr), T, E, _vp(counts), _vp(eo), _vp(to), _vp(st), _vp(sg),
                                    _vp(ts), cap, _vp(workspace), rwsb, int(k_target), float(momentum),
