@@ -149,8 +149,8 @@ def threshold_dynamics(et, W, dev, stream, workload: str, seed: int) -> dict:
     if not torch.equal(thr, thr_eager):
         raise RuntimeError("graph-replayed threshold dynamics differ from the eager loop")
     del graph
-    # The same loop through et_route_update: the update's selection runs on the
-    # library's second stream beside the routing, the EMA write after both.
+    # The same loop through et_route_update (routing, then the EMA update, in
+    # one call).
     def combined():
         for i in range(steps):
             et.route_update(logits[i], thr, cfg["k_target"], cfg["momentum"], slot_capacity=cap, stat=stat,
@@ -818,8 +818,8 @@ def main() -> int:
             print(f"  C5 threshold dynamics: {dyn['steps']} steps, route {dyn['route_ms']:.4f} ms + EMA update "
                   f"{dyn['ema_update_ms']:.4f} ms per step, mean k {dyn['mean_k_first_step']} -> "
                   f"{dyn['mean_k_last_step']}; all steps replayed as one HIP graph "
-                  f"{dyn['graph_replay_ms_per_step']:.4f} ms per step; et_route_update (the update beside the "
-                  f"routing) {dyn['route_update_ms']:.4f} ms per step, {dyn['route_update_graph_replay_ms_per_step']:.4f} "
+                  f"{dyn['graph_replay_ms_per_step']:.4f} ms per step; et_route_update (routing and update in one call) "
+                  f"{dyn['route_update_ms']:.4f} ms per step, {dyn['route_update_graph_replay_ms_per_step']:.4f} "
                   f"ms replayed", file=sys.stderr, flush=True)
             if step.act == torch.bfloat16 and E <= 256:
                 rp = router_producer(et, dev, stream, step.X, E)

@@ -43,10 +43,9 @@
  *    dlogits is 0 at dropped pairs, and the rows of dropped slots below the
  *    capacity are left as they were (their dgate is 0 or left as it was).
  *  - Concurrent calls on different streams are safe when their buffers are
- *    disjoint.  Two entry points hold device state: et_route_noalloc's static
- *    scratch (one per GPU, shared by its calls) and et_route_update's side
- *    stream (one per GPU, used only under HIP graph capture, serialised by a
- *    mutex); every other entry point keeps none.
+ *    disjoint.  One entry point holds device state: et_route_noalloc's static
+ *    scratch (one per GPU, shared by its calls); every other entry point
+ *    keeps none.
  */
 #ifndef ETMOE_H
 #define ETMOE_H
@@ -225,15 +224,8 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
 /*
  * Routing and the EMA threshold update of one training batch in one call:
  * the results of et_route (with the thresholds from before the update)
- * followed by et_threshold_update, bit for bit.  Issued eagerly it enqueues
- * exactly those two calls' kernels on `stream`.  While `stream` is being
- * captured into a HIP graph, the update's selection (which reads only the
- * logits) goes on a second HIP stream of the library's (one per device,
- * default priority, created on the first such call), a parallel branch beside
- * the routing; `stream` then joins it (HIP events) and applies the EMA, so
- * the captured work still ends on `stream`.  If that side stream already
- * belongs to another capture (another host thread, or an earlier call of the
- * same capture), the call falls back to the single-stream order.
+ * followed by et_threshold_update, bit for bit.  It enqueues exactly those
+ * two calls' kernels on `stream`, in that order.
  * Workspaces: route_workspace as et_route's, thr_workspace as
  * et_threshold_update's; their byte ranges must not overlap
  * (ET_ERR_INVALID_ARGUMENT).

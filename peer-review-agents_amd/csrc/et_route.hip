@@ -616,10 +616,10 @@ __device__ __forceinline__ int rank_below_plus(uint64_t m, int base)
 
 // One walk of a wave over its route group.  EXACT = false decides every
 // selection by the logit bounds and gives up (returns true, leaving the group
-// unfinished) when a batch holds a logit between an expert's bounds (or NaN)
-// or a token with no expert; it evaluates no sigmoid.  EXACT = true evaluates
-// the exact score where the bounds do not decide, takes the argmax fallback,
-// and always finishes.  FULL: the group has all kPairGroup tokens (no bound
+// unfinished) when a batch holds a logit between an expert's bounds (or NaN);
+// it evaluates sigmoids only for the argmax fallback of a token with no
+// expert.  EXACT = true evaluates the exact score where the bounds do not
+// decide, and always finishes.  Both take the fallback on exact scores.  FULL: the group has all kPairGroup tokens (no bound
 // checks).  The list (two words per entry) is flushed to `gp` in whole chunks
 // of 64 entries as it fills.  info[g] runs as (e << kInfoExpert) + (count so
 // far).  With GM <= 2 every expert group exists (G == GM).
@@ -639,7 +639,6 @@ __device__ __forceinline__ bool route_walk(const float* __restrict__ logits, int
     for (int ub = 0; ub < nu; ub += UT) {
         if (ub != 0 || (EXACT && UT < kPairGroup)) load_logits_raw<GM, UT>(logits, E, G, t0 + ub, t0 + nu, lg);
         uint64_t ambm = 0ull;     // lanes that met an ambiguous logit in the batch
-        int zero_k = 0;           // a token of the batch took no expert
 #pragma unroll
         for (int u = 0; u < UT; ++u) {
             if (!FULL && ub + u >= nu) break;
@@ -667,16 +666,15 @@ __device__ __forceinline__ bool route_walk(const float* __restrict__ logits, int
                     k += (int)__popcll(mm[g]);
                 }
             }
-            if (EXACT) {
-                if (k == 0) {
-                    float sc[GM];
+            if (k == 0) {
+                // the argmax fallback on exact scores (in the bounds walk too:
+                // if the batch also met an ambiguous logit, the exact walk
+                // redoes the group)
+                float sc[GM];
 #pragma unroll
-                    for (int g = 0; g < GM; ++g) sc[g] = ve[g] ? sigmoid(lg[u][g]) : __builtin_nanf("");
-                    select_fallback<GM>(sc, G, mm);
-                    k = 1;
-                }
-            } else {
-                zero_k |= k == 0 ? 1 : 0;
+                for (int g = 0; g < GM; ++g) sc[g] = ve[g] ? sigmoid(lg[u][g]) : __builtin_nanf("");
+                select_fallback<GM>(sc, G, mm);
+                k = 1;
             }
             int below = pend;
 #pragma unroll
@@ -705,7 +703,7 @@ __device__ __forceinline__ bool route_walk(const float* __restrict__ logits, int
                 pend -= full;
             }
         }
-        if (!EXACT && (ambm != 0ull || zero_k != 0)) return true;
+        if (!EXACT && ambm != 0ull) return true;
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     if (lane < pend) gp[(lp - pend) + lane] = reinterpret_cast<const u32x2_t*>(list)[lane];

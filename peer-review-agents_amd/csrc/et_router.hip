@@ -455,8 +455,13 @@ __global__ __launch_bounds__(MW * kWave) void router_logits_kernel(
             if (nmain + r < nchunks) step(nmain + r, r);
 
         // wait until the last products are written (at most 16 passes of 4
-        // cycles after issue; 80 cycles of s_nop)
+        // cycles after issue; 80 cycles of s_nop).  The MFMAs are inline asm,
+        // so the compiler's hazard recognizer does not see them: the
+        // scheduling barriers on both sides keep every read of the
+        // accumulators (v_accvgpr_read, or a VALU use) after the nops.
+        __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         // epilogue: lane l writes expert n * M + l % M of its token rows per tile
         if (!ROUTE || logits != nullptr) {
 #pragma unroll

@@ -630,10 +630,8 @@ def route_update(logits: torch.Tensor, thr: torch.Tensor, k_target: int, momentu
                  thr_workspace: Optional[torch.Tensor] = None) -> RoutingPlan:
     """Routing with the current thresholds, then the EMA update of thr from
     the same batch, in one call: the same results as :func:`route` followed by
-    :func:`threshold_update_` (et_route_update).  Issued eagerly it enqueues
-    exactly those two calls' kernels on the current stream; captured into a
-    HIP graph, the update's selection becomes a parallel branch beside the
-    routing, which shortens the replayed step."""
+    :func:`threshold_update_` (et_route_update), whose kernels it enqueues on
+    the current stream in that order."""
     _require(logits, "logits", torch.float32, 2)
     dev = logits.device
     T, E = logits.shape

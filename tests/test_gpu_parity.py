@@ -386,8 +386,8 @@ def _plans_identical(a, b):
 @pytest.mark.parametrize("T,E,k,cap", [(8192, 64, 8, None), (1, 4, 2, None), (5000, 128, 8, "under"),
                                        (131072, 64, 8, "exact"), (300, 1024, 16, None), (999, 7, 3, None)])
 def test_route_update_matches_route_then_update(et, orc, dev, T, E, k, cap):
-    """et_route_update (the update's selection on a second stream) equals
-    route followed by threshold_update_ bit for bit, and the oracle."""
+    """et_route_update equals route followed by threshold_update_ bit for
+    bit, and the oracle."""
     print(f"route_update T={T} E={E} k={k} cap={cap}", flush=True)
     rng = np.random.default_rng([T, E, 5])
     lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
@@ -413,16 +413,14 @@ def test_route_update_matches_route_then_update(et, orc, dev, T, E, k, cap):
 
 
 def test_route_update_graph_replay(et, dev):
-    """et_route_update captured in a HIP graph (its side stream joins the
-    capture): three replays, with eager work and synchronisation between
-    them, each bit-identical to the eager route + update it replaces."""
+    """et_route_update captured in a HIP graph: three replays, with eager
+    work and synchronisation between them, each bit-identical to the eager
+    route + update it replaces."""
     T, E, k, m = 16384, 64, 8, 0.99
     g = torch.Generator(device=dev)
     g.manual_seed(21)
     L = torch.randn(T, E, generator=g, device=dev)
     cap = T * E
-    warm = torch.full((E,), 0.9, device=dev)
-    et.route_update(L, warm, k, m, slot_capacity=cap)     # creates the library's side stream outside capture
     torch.cuda.synchronize()
     thr_g = torch.full((E,), 0.9, device=dev)
     thr_e = thr_g.clone()

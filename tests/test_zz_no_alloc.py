@@ -2,7 +2,8 @@
 no device allocation) against et_route with a caller workspace, through the
 C ABI: every output bit-identical, on two calls in a row where the second has
 fewer tokens and experts (the scratch keeps the first call's contents, and
-nothing in it needs clearing), then a third call at C3's full routing shape."""
+nothing in it needs clearing), then a third call at C3's full routing shape,
+and the call captured into a HIP graph and replayed."""
 import ctypes
 import importlib
 
@@ -34,6 +35,42 @@ def _call(lib, name, lg, thr, out, cap, ws=None):
         args += [vp(ws), ws.numel()]
     rc = getattr(lib, name)(*args, stream)
     assert rc == 0, lib.et_last_error().decode()
+
+
+def test_route_noalloc_graph_capture(et, dev):
+    """et_route_noalloc captured in a HIP graph (in a fresh process this is
+    its first call, so the scratch address is looked up during the capture):
+    two replays, with eager work and synchronisation between them, each
+    bit-identical to an eager et_route with a caller workspace."""
+    lib = et.lib()
+    T, E = 8192, 64
+    print(f"route_noalloc graph: T={T} E={E}", flush=True)
+    rng = np.random.default_rng([T, E, 3])
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    thr = np.full(E, 0.8, np.float32)
+    L, TH = torch.from_numpy(lg).to(dev), torch.from_numpy(thr).to(dev)
+    cap = T * E
+    ws = torch.empty(et.route_workspace_bytes(T, E), dtype=torch.uint8, device=dev)
+    a, b = _outputs(T, E, cap, dev), _outputs(T, E, cap, dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _call(lib, "et_route_noalloc", L, TH, b, cap)
+    for rep in range(2):
+        for f in FIELDS:
+            b[f].fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        _call(lib, "et_route", L, TH, a, cap, ws)
+        torch.cuda.synchronize()
+        S = int(a["expert_offsets"][E])
+        assert S > 0 and int(b["expert_offsets"][E]) == S, rep
+        for f in FIELDS:
+            x, y = a[f], b[f]
+            if f in ("sorted_token", "slot_gate", "token_slot"):
+                x, y = x[:S], y[:S]
+            assert torch.equal(x.view(torch.int32), y.view(torch.int32)), (rep, f)
+    del graph
 
 
 @pytest.mark.parametrize("shapes", [((4096, 100), (777, 37)), ((65536, 128), (1000, 8))])
