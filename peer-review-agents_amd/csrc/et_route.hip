@@ -885,10 +885,19 @@ __global__ __launch_bounds__(kScanThreads) void route_segscan_kernel(
 // per expert and first token-major index (its prefix within its segment plus
 // the earlier segments) -- and leaves it in LDS; each wave then adds the
 // counts of the tile's earlier groups (also through LDS), keeps its current
-// group's first slot per expert in an LDS table, and writes the group's pairs
+// group's first slot per expert in an LDS table, and places the group's pairs
 // 64 at a time.  Every independent load of a wave (its groups' counts and
 // slot totals, their first 64 list entries) goes out first.
+// Token-major outputs (token_slot, token_offsets) are written as the pairs
+// are placed.  The slot-indexed ones (sorted_token, slot_gate) are staged in
+// LDS in the tile's own expert-major order -- expert e's pairs of the tile
+// are its slots [tbase[e], tbase[e] + n_e), at stage positions [loff[e],
+// loff[e] + n_e) with loff the exclusive scan of the tile's expert counts --
+// and written out by the whole block with lane = stage position, so one store
+// instruction covers a few contiguous runs of slots rather than 64 scattered
+// ones.  A tile with more than kStage pairs writes them directly.
 constexpr int kPlaceGroups = 2;
+constexpr int kStage = 2048;
 constexpr int kXcds = 8;           // accelerator complex dies of an MI355X
 
 template <int GM>
@@ -896,7 +905,8 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
     const u32x2_t* __restrict__ pairs, int T, int E, int gpt, int PG, int S, int RS,
     const int32_t* __restrict__ seg_counts, const int32_t* __restrict__ seg_slots,
     const uint8_t* __restrict__ group_counts, const int32_t* __restrict__ block_base,
-    const int32_t* __restrict__ group_slots, const int32_t* __restrict__ block_slot_base, int32_t* __restrict__ counts,
+    const int32_t* __restrict__ group_slots, const int32_t* __restrict__ block_slot_base,
+    const int32_t* __restrict__ block_counts, const int32_t* __restrict__ block_slots, int32_t* __restrict__ counts,
     int32_t* __restrict__ expert_offsets, int32_t* __restrict__ token_offsets, int32_t* __restrict__ sorted_token,
     float* __restrict__ slot_gate, int32_t* __restrict__ token_slot, int64_t cap)
 {
@@ -912,10 +922,18 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
                                     : (int)blockIdx.x;
     const int g0 = PG * wave;                       // the wave's first group within the tile
     const int G = (E + kWave - 1) / kWave;
+    const int nwave = (int)blockDim.x / kWave;
     int* red = lds_i;                               // [gpt][E] group counts, then [gpt] slot totals
     int* tbase = lds_i + gpt * (E + 1);             // [E] the tile's first slot per expert, then [1] token-major
-    int* ptab = tbase + E + 1 + wave * E;           // the current group's first slot per expert
+    int* loff = tbase + E + 1;                      // [E] the tile's expert-major stage offsets
+    int2* ptab0 = reinterpret_cast<int2*>(lds_i + ((loff + E - lds_i + 1) & ~1));   // (8-byte aligned)
+    int2* ptab = ptab0 + wave * E;                  // the current group's (first slot, stage position)
+    int* st_slot = reinterpret_cast<int*>(ptab0 + nwave * E);   // [kStage] stage
+    int* st_tok = st_slot + kStage;
+    float* st_gate = reinterpret_cast<float*>(st_tok + kStage);
     const int gp_last = kPairGroup * E - 1;
+    const int tile_pairs = block_slots[b];
+    const bool staged = tile_pairs <= kStage;       // block-uniform
 
     int cnt_q[kPlaceGroups][GM], lp[kPlaceGroups];
     u32x2_t pr[kPlaceGroups];
@@ -931,10 +949,11 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
 
     if (wave == 0) {
         const int seg = b / RS;
-        int cnt_e[GM], bb[GM];
+        int cnt_e[GM], bb[GM], tc[GM];
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
             bb[g] = block_base[(int64_t)b * E + min(min(g, G - 1) * kWave + lane, E - 1)];
+            tc[g] = block_counts[(int64_t)b * E + min(min(g, G - 1) * kWave + lane, E - 1)];
             cnt_e[g] = 0;
         }
         int tile_slot_base = block_slot_base[b];
@@ -960,7 +979,7 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
                 }
             }
         }
-        int run = 0;
+        int run = 0, lrun = 0;
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
             const int e = g * kWave + lane;
@@ -969,6 +988,10 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
             const int incl = wave_incl_scan(c);
             const int eo = run + incl - c;
             run += __builtin_amdgcn_readlane(incl, kWave - 1);
+            const int n = ve ? tc[g] : 0;
+            const int lincl = wave_incl_scan(n);
+            if (ve) loff[e] = lrun + lincl - n;
+            lrun += __builtin_amdgcn_readlane(lincl, kWave - 1);
             if (ve) tbase[e] = eo + bb[g];
             if (ve && b == 0) {
                 expert_offsets[e] = eo;
@@ -995,14 +1018,17 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
         }
     }
     __syncthreads();
-    int base[GM];
+    int base[GM], lbase[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
         const int e = g * kWave + lane;
         base[g] = 0;
+        lbase[g] = 0;
         if (g < G && e < E) {
-            base[g] = tbase[e];
-            for (int i = 0; i < g0; ++i) base[g] += red[i * E + e];
+            int pre = 0;
+            for (int i = 0; i < g0; ++i) pre += red[i * E + e];
+            base[g] = tbase[e] + pre;
+            lbase[g] = loff[e] + pre;
         }
     }
     int tok_pos = tbase[E];
@@ -1018,8 +1044,9 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
             const int e = g * kWave + lane;
-            if (g < G && e < E) ptab[e] = base[g];
+            if (g < G && e < E) ptab[e] = make_int2(base[g], lbase[g]);
             base[g] += cnt_q[j][g];
+            lbase[g] += cnt_q[j][g];
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         u32x2_t nx = pr[j];
@@ -1034,16 +1061,33 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
             if (jj < lp[j]) {
                 // a token's first pair gives its offset
                 if (u != (lane == 0 ? u_prev : u_left)) token_offsets[t0 + u] = tok_pos + jj;
-                const int slot = ptab[info >> kInfoExpert] + (int)(info & ((1u << kInfoTok) - 1u));
+                const int2 pt = ptab[info >> kInfoExpert];
+                const int occ = (int)(info & ((1u << kInfoTok) - 1u));
+                const int slot = pt.x + occ;
                 if ((int64_t)tok_pos + jj < cap) token_slot[tok_pos + jj] = slot;
-                if ((int64_t)slot < cap) {
+                const float gate = sigmoid(u2f(cur.x));
+                if (staged) {
+                    const int at = pt.y + occ;
+                    st_slot[at] = slot;
+                    st_tok[at] = (int)(t0 + u);
+                    st_gate[at] = gate;
+                } else if ((int64_t)slot < cap) {
                     sorted_token[slot] = (int)(t0 + u);
-                    slot_gate[slot] = sigmoid(u2f(cur.x));
+                    slot_gate[slot] = gate;
                 }
             }
             u_prev = __builtin_amdgcn_readlane(u, kWave - 1);
         }
         tok_pos += lp[j];
+    }
+    if (!staged) return;
+    __syncthreads();
+    for (int i = (int)threadIdx.x; i < tile_pairs; i += (int)blockDim.x) {
+        const int slot = st_slot[i];
+        if ((int64_t)slot < cap) {
+            sorted_token[slot] = st_tok[i];
+            slot_gate[slot] = st_gate[i];
+        }
     }
 }
 
@@ -1186,11 +1230,11 @@ static int route_pairs_path(const float* logits, const float* thr, int64_t T, in
     ET_SWITCH_GROUPS(p.G, {
         const int PG = gpt >= kPlaceGroups ? kPlaceGroups : 1;
         const int nwave = gpt / PG;
-        const size_t lds = (size_t(gpt) * (E + 1) + E + 1 + size_t(nwave) * E) * 4;
+        const size_t lds = (size_t(gpt) * (E + 1) + 2 * size_t(E) + 2 + 2 * size_t(nwave) * E + 3 * kStage) * 4;
         route_place_kernel<GM><<<dim3(NB), dim3(nwave * kWave), lds, s>>>(
             ws.pairs, Ti, Ei, gpt, PG, S, RS, ws.seg_counts, ws.seg_slots, ws.group_counts, ws.block_base,
-            ws.group_slots, ws.block_slot_base, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
-            token_slot, slot_capacity);
+            ws.group_slots, ws.block_slot_base, ws.block_counts, ws.block_slots, counts, expert_offsets,
+            token_offsets, sorted_token, slot_gate, token_slot, slot_capacity);
     });
     return check_launch("route_place_kernel");
 }
