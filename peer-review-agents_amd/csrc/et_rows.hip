@@ -208,6 +208,7 @@ __global__ __launch_bounds__(kRowThreads) void dispatch_fwd_elem(
 // ---------------------------------------------------------------------------
 
 constexpr int kGatherWaves = 2;
+constexpr int kGatherBatch = 8;     // slots whose loads a gather wave issues together
 
 // ROUTER (dispatch backward only): every slot also adds dl * W[e] with the
 // slot's router-logit gradient dl and expert e, read per token-list entry
@@ -230,6 +231,40 @@ __global__ __launch_bounds__(kGatherWaves * kWave) void combine_fwd_vec(
     float acc[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) acc[i] = 0.0f;
+    if constexpr (!ROUTER) {
+        // Batches of kGatherBatch slots: every load of a batch (rows and
+        // gates) is issued before the first is used, then the batch is
+        // accumulated in list order, skipping invalid slots as one at a time.
+        for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
+            const int my = load_slot_block(tok_slot, jb, sp.j1);
+            const int n = min(kWave, sp.j1 - jb);
+            for (int u0 = 0; u0 < n; u0 += kGatherBatch) {
+                v4u w[kGatherBatch];
+                float g[kGatherBatch];
+                bool ok[kGatherBatch];
+#pragma unroll
+                for (int i = 0; i < kGatherBatch; ++i) {
+                    const int s = __builtin_amdgcn_readlane(my, min(u0 + i, n - 1));
+                    ok[i] = u0 + i < n && s >= 0 && (int64_t)s < cap;
+                    const int sc = ok[i] ? s : 0;
+                    w[i] = v4u{0u, 0u, 0u, 0u};
+                    if (ok[i] && on) w[i] = ld16_nt(yp + (int64_t)sc * rb + idx * 16);
+                    g[i] = GATE && ok[i] ? gate[sc] : 1.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < kGatherBatch; ++i) {
+                    if (ok[i] && on) {
+                        float f[N];
+                        P::unpack(w[i], f);
+#pragma unroll
+                        for (int c = 0; c < N; ++c) acc[c] = __builtin_fmaf(g[i], f[c], acc[c]);
+                    }
+                }
+            }
+        }
+        if (on) st16_nt(y + (int64_t)sp.t * rb + idx * 16, P::pack(acc));
+        return;
+    }
     for (int jb = sp.j0; jb < sp.j1; jb += kWave) {
         const int my = load_slot_block(tok_slot, jb, sp.j1);
         const int n = min(kWave, sp.j1 - jb);
