@@ -146,14 +146,23 @@ __device__ __forceinline__ void hist_flush(const uint32_t* h, uint32_t* __restri
 // Histogram pass: the digit of every key of the block's tokens.  Each wave
 // takes UT consecutive tokens at a time with all UT loads issued before the
 // first use (addresses clamped into the matrix).
+//   The digit is found in the logit domain, as routing decides selection:
+// digit d holds the scores in [d / kBins, (d + 1) / kBins), so with the logit
+// bounds of select_bounds, a logit l with hi(d / kBins) <= l and l <=
+// lo((d + 1) / kBins) has digit d (the score's order is monotone up to 2
+// steps, which those bounds allow for).  The block puts the pairs
+// (hi(d / kBins), lo((d + 1) / kBins)) of every d in LDS while its first loads
+// are in flight; a lane then takes d from a fast approximate sigmoid and
+// checks it against its pair, and only a lane whose check fails (a logit near
+// a digit edge or NaN: rare) evaluates the exact key.  So the digits are
+// exactly those of score_digit(score_key(l)).
 template <int UT>
 __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(const float* __restrict__ logits, int T, int E,
                                                                 int tpb, uint32_t* __restrict__ partial)
 {
     __shared__ uint32_t h[kBinWords * kPitch];
+    __shared__ float2 dtab[kBins];
     const int tid = threadIdx.x;
-    for (int i = tid; i < kBinWords * kPitch; i += kHistThreads) h[i] = 0u;
-    __syncthreads();
     const int lane = lane_id();
     const int wave = tid >> 6;
     const int e = blockIdx.y * kWave + lane;
@@ -161,14 +170,43 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(const float* __r
     const int ec = min(e, E - 1);
     const int64_t t0 = (int64_t)blockIdx.x * tpb;
     const int64_t t1 = min((int64_t)T, t0 + tpb);
-    for (int64_t tb = t0 + (int64_t)wave * UT; tb < t1; tb += (int64_t)kHistWaves * UT) {
-        float v[UT];
+    // the wave's first batch of loads, then the LDS set-up under them
+    int64_t tb = t0 + (int64_t)wave * UT;
+    float v[UT];
+    if (tb < t1) {
 #pragma unroll
         for (int u = 0; u < UT; ++u) v[u] = logits[min(tb + u, t1 - 1) * E + ec];
+    }
+    for (int i = tid; i < kBinWords * kPitch; i += kHistThreads) h[i] = 0u;
+    if (tid < kBins) {
+        // thread b: the bounds of the score b / kBins (hi(0) = -inf); the
+        // last digit also holds the score 1, so nothing bounds it above
+        float hi, lo;
+        select_bounds(bin_edge((uint32_t)tid), hi, lo);
+        dtab[tid].x = hi;
+        if (tid > 0) dtab[tid - 1].y = lo;
+        if (tid == kBins - 1) dtab[tid].y = __builtin_huge_valf();
+    }
+    __syncthreads();
+    for (; tb < t1; tb += (int64_t)kHistWaves * UT) {
+        if (tb != t0 + (int64_t)wave * UT) {
+#pragma unroll
+            for (int u = 0; u < UT; ++u) v[u] = logits[min(tb + u, t1 - 1) * E + ec];
+        }
 #pragma unroll
         for (int u = 0; u < UT; ++u) {
             if (!ve || tb + u >= t1) continue;
-            hist_add(h, score_digit(score_key(v[u])), lane);
+            const float l = v[u];
+            // approximate digit (a NaN converts to 0 and fails the check)
+            const float sa = __builtin_amdgcn_rcpf(1.0f + __expf(-l));
+            const uint32_t da = min((uint32_t)(sa * (float)kBins), (uint32_t)kBins - 1u);
+            const float2 b = dtab[da];
+            const bool ok = l >= b.x && l <= b.y;
+            uint32_t d = da;
+            if (__ballot(!ok) != 0ull) {         // (skipped by the whole wave when every check holds)
+                if (!ok) d = score_digit(score_key(l));
+            }
+            hist_add(h, d, lane);
         }
     }
     __syncthreads();
