@@ -371,6 +371,45 @@ def test_threshold_update_ties(et, orc, dev, T, E, k):
     np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
 
 
+def test_threshold_update_logits_at_digit_edges(et, orc, dev):
+    """The histogram pass takes each score's digit floor(score * 256) from a
+    fast sigmoid checked against logit bounds of the digit edges b / 256, and
+    the collect pass skips logits outside the chosen digit's bounds; only
+    logits near an edge take the exact score.  Here most logits sit within
+    40 float steps of the logit of an edge (a different edge per column, and
+    in the last columns many columns' statistic falls inside such a crowd),
+    with NaN and +-inf mixed in: statistic and thresholds bit-exact."""
+    T, E, k = 8192, 64, 8
+    rng = np.random.default_rng(31)
+    edges = rng.integers(1, 256, size=E)
+    l0 = np.log(edges / 256.0) - np.log1p(-edges / 256.0)          # logit of b / 256
+    l0 = l0.astype(np.float32)
+    target = np.repeat(l0[None, :], T, 0)
+    steps = rng.integers(-40, 41, size=(T, E))
+    for s_ in range(1, 41):
+        up, dn = steps >= s_, steps <= -s_
+        target[up] = np.nextafter(target[up], np.float32(np.inf))
+        target[dn] = np.nextafter(target[dn], np.float32(-np.inf))
+    lg = target
+    # a quarter of each column is randn, so the c-th largest lands in the crowd
+    # for some columns and outside it for others
+    mix = rng.random((T, E)) < 0.25
+    lg[mix] = (rng.standard_normal(int(mix.sum())) * 2).astype(np.float32)
+    lg[rng.random((T, E)) < 0.01] = np.nan
+    lg[rng.random((T, E)) < 0.005] = np.inf
+    lg[rng.random((T, E)) < 0.005] = -np.inf
+    lg = np.ascontiguousarray(lg, np.float32)
+    thr0 = rng.random(E).astype(np.float32)
+    thr_o, stat_o = orc.threshold_update(lg, thr0, k, 0.99)
+    thr = dev_f32(thr0, dev)
+    stat = et.threshold_update_(thr, dev_f32(lg, dev), k, 0.99)
+    np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+    np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
+    # the statistic of most columns lies in the crowd at the edge
+    at_edge = np.abs(stat_o - edges / 256.0) < 1e-4
+    assert at_edge.sum() >= E // 4
+
+
 def _plans_identical(a, b):
     """Routing outputs equal bit for bit; the slot arrays up to min(S,
     capacity) (past it they hold whatever the buffer held)."""
