@@ -5,16 +5,18 @@
 // et_route (the pair-list path) reads the logits once, in three launches:
 //   1. count (route_pairs_kernel): a wave walks a route group of 8 tokens with
 //      lane = expert; selection is decided against per-expert logit bounds
-//      (no sigmoid), and every routed pair is listed in token order with its
-//      logit and its (token, occurrence, expert) indices; per-group expert
-//      counts and slot totals, and their tile sums, follow.
+//      (a sigmoid only between the bounds and for the argmax fallback), and
+//      every routed pair is listed in token order with its logit and its
+//      (token, occurrence, expert) indices; per-group expert counts and slot
+//      totals, and their tile sums, follow.
 //   2. segmented scan (route_segscan_kernel): the tile sums' exclusive prefix
 //      within segments of up to 256 tiles, and the segment totals.
 //   3. place (route_place_kernel): lane = pair; each pair's slot is its
 //      expert's first slot in its group plus its occurrence index, its gate the
 //      sigmoid of its logit, and a token's offset the list index of its first
-//      pair.  Expert slots come out in token order (stable), token-major
-//      entries in ascending expert order.
+//      pair; the slot-indexed outputs go out through an LDS stage in the
+//      tile's expert-major order.  Expert slots come out in token order
+//      (stable), token-major entries in ascending expert order.
 // et_route_noalloc (the two-read path) keeps the older count / scan / fill
 // kernels, whose workspace is O(E) per block and fits a small static scratch:
 // the count and fill passes each read the logits, with lane = expert.

@@ -4,11 +4,12 @@
 //
 // Scores are ordered by their bit pattern, the key (a NaN score keys as 0; a
 // score is in [0, 1], so a key is at most f2u(1.0)).  Four launches:
-//   histogram pass: reads the logits, computes every score once and counts
-//     its digit floor(score * 256) (255 for a score of 1, 0 for NaN) per
-//     expert.  The digit is a monotone function of the key that spreads
-//     scores over [0, 1] evenly, where the key's top bits would spend most of
-//     their values on the exponent.
+//   histogram pass: reads the logits and counts each score's digit
+//     floor(score * 256) (255 for a score of 1, 0 for NaN) per expert, taken
+//     from a fast sigmoid checked against per-digit logit bounds (the exact
+//     score only where the check fails).  The digit is a monotone function of
+//     the key that spreads scores over [0, 1] evenly, where the key's top
+//     bits would spend most of their values on the exponent.
 //   bin select (one block per expert): sums the blocks' histograms, finds the
 //     digit bin that holds the c-th largest key and the rank left inside it,
 //     and turns the bin's two score edges into logit bounds (select_bounds).
