@@ -1245,10 +1245,24 @@ static int route_pairs_path(const float* logits, const float* thr, int64_t T, in
 
 using namespace et;
 
+// The pair lists reserve room for every (token, expert) pair (8 bytes each),
+// so above kPairWsLimit bytes of workspace et_route takes the two-read kernels
+// instead: the same outputs bit for bit, from a workspace of O(E) per block.
+constexpr size_t kPairWsLimit = size_t(1) << 30;
+
+static size_t pair_ws_bytes(int64_t T, int64_t E) { return pair_ws_layout(nullptr, pair_plan(T, E), T, E).bytes; }
+static size_t two_read_ws_bytes(int64_t T, int64_t E) { return route_ws_layout(nullptr, route_plan(T, E), E).bytes; }
+static bool use_pairs(int64_t T, int64_t E) { return pair_ws_bytes(T, E) <= kPairWsLimit; }
+
+static int route_two_read(const float* logits, const float* thr, int64_t T, int64_t E, int32_t* counts,
+                          int32_t* expert_offsets, int32_t* token_offsets, int32_t* sorted_token, float* slot_gate,
+                          int32_t* token_slot, int64_t slot_capacity, void* workspace, hipStream_t s);
+
 extern "C" size_t et_route_workspace_bytes(int64_t num_tokens, int64_t num_experts)
 {
     if (num_tokens < 0 || num_experts < 1) return 0;
-    return pair_ws_layout(nullptr, pair_plan(num_tokens, num_experts), num_tokens, num_experts).bytes;
+    return use_pairs(num_tokens, num_experts) ? pair_ws_bytes(num_tokens, num_experts)
+                                              : two_read_ws_bytes(num_tokens, num_experts);
 }
 
 // Argument checks shared by et_route and et_route_noalloc (no HIP call).
@@ -1282,19 +1296,24 @@ extern "C" int et_route(const float* logits, const float* thr, int64_t T, int64_
                              slot_gate, token_slot, slot_capacity))
         return rc;
     if (!workspace) return fail(ET_ERR_INVALID_ARGUMENT, "et_route: null workspace pointer");
+    const size_t need = et_route_workspace_bytes(T, E);
+    if (workspace_bytes < need)
+        return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_route: workspace needs " + std::to_string(need) +
+                                                    " bytes, got " + std::to_string(workspace_bytes));
+    if (!use_pairs(T, E))
+        return route_two_read(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
+                              token_slot, slot_capacity, workspace, static_cast<hipStream_t>(stream));
     const PairPlan p = pair_plan(T, E);
     const PairWs ws = pair_ws_layout(workspace, p, T, E);
-    if (workspace_bytes < ws.bytes)
-        return fail(ET_ERR_WORKSPACE_TOO_SMALL, "et_route: workspace needs " + std::to_string(ws.bytes) +
-                                                    " bytes, got " + std::to_string(workspace_bytes));
     return route_pairs_path(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                             token_slot, slot_capacity, p, ws, static_cast<hipStream_t>(stream));
 }
 
-// The two-read routing (et_route_noalloc's path): a count pass and a fill
-// pass that both read the logits, with a workspace of per-wave and per-block
-// counts only (O(E) per block, so it fits a small static scratch at any T).
-// Outputs bit-identical to et_route's.
+// The two-read routing (et_route_noalloc's path, and et_route's where the
+// pair lists would exceed kPairWsLimit): a count pass and a fill pass that
+// both read the logits, with a workspace of per-wave and per-block counts only
+// (O(E) per block, so it fits a small static scratch at any T).  Outputs
+// bit-identical to the pair path's.
 static int route_two_read(const float* logits, const float* thr, int64_t T, int64_t E, int32_t* counts,
                           int32_t* expert_offsets, int32_t* token_offsets, int32_t* sorted_token, float* slot_gate,
                           int32_t* token_slot, int64_t slot_capacity, void* workspace, hipStream_t s)

@@ -34,6 +34,12 @@ def test_workspace_sizes(et):
     assert lib.et_route_workspace_bytes(65536, 128) >= 2 * 256 * 128 * 4
     assert lib.et_route_workspace_bytes(0, 8) > 0
     assert lib.et_route_workspace_bytes(10, 0) == 0
+    # the pair lists hold room for every (token, expert) pair, 8 bytes each;
+    # past 1 GiB of them et_route takes the two-read kernels, whose workspace
+    # is O(E) per block
+    assert lib.et_route_workspace_bytes(65536, 128) >= 65536 * 128 * 8
+    assert lib.et_route_workspace_bytes(540000, 256) < (64 << 20)
+    assert lib.et_route_workspace_bytes(2 ** 21, 1023) < (64 << 20)
     assert lib.et_threshold_workspace_bytes(131072, 64) >= 64 * 256 * 4 + 131072 * 64 * 4
     assert lib.et_threshold_workspace_bytes(10, 0) == 0
 

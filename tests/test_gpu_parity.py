@@ -106,6 +106,23 @@ def test_route_synthetic_bit_exact(et, orc, dev, T, E, mode):
     assert_route_equal(plan, orc.route(lg, thr))
 
 
+def test_route_large_batch_takes_the_two_read_kernels(et, orc, dev):
+    """T = 540000, E = 256: the pair lists would exceed 1 GiB, so et_route
+    takes the count and fill kernels with a small workspace; routing still
+    bit-exact with the oracle (quantile thresholds, NaN logits, fallback
+    tokens)."""
+    T, E = 540_000, 256
+    print(f"route two-read T={T} E={E}", flush=True)
+    assert et.route_workspace_bytes(T, E) < (64 << 20)
+    rng = np.random.default_rng([T, E])
+    lg = rng.standard_normal((T, E), dtype=np.float32)
+    lg[::9973] = -30.0                                   # tokens that clear no threshold
+    lg[rng.random((T, E)) < 1e-4] = np.nan
+    thr = np.full(E, 0.93, np.float32)
+    plan = et.route(dev_f32(lg, dev), dev_f32(thr, dev))
+    assert_route_equal(plan, orc.route(lg, thr))
+
+
 def test_route_empty_batch(et, dev):
     plan = et.route(torch.zeros(0, 8, device=dev), torch.full((8,), 0.5, device=dev))
     assert plan.num_slots == 0
