@@ -11,7 +11,9 @@ quantile thresholds, all-fallback, all-selected, NaN/inf/tie specials); sizes
 are kept small enough for the oracle to finish in well under a second.  Those
 shapes all walk combine backward's slots in plain slot order (dY <= 16 MiB), so
 a second set draws shapes above that size with more than 1.25 slots per token,
-which take the token-window walk."""
+which take the token-window walk.  A third set draws wider routing shapes (T up
+to 20000, E up to 1024) and threshold regimes, logits at the thresholds
+included, for routing and the EMA update alone."""
 import numpy as np
 import pytest
 import torch
@@ -130,3 +132,62 @@ def test_random_shape_windowed_combine_backward(et, orc, dev, seed):
     assert torch.equal(iv(dyp_b[:S]), iv(dyp_g))
     assert torch.equal(dgate_b[:S].view(torch.int32), dgate_g.view(torch.int32))
     assert torch.equal(dl_b.view(torch.int32), dl_g.view(torch.int32))
+
+
+# --------------------------------------------------------------------------- #
+# routing and the EMA update alone, over wider shapes
+# --------------------------------------------------------------------------- #
+
+R_E_CHOICES = [1, 4, 7, 8, 31, 64, 65, 128, 200, 256, 400, 512, 777, 1024]
+
+
+def route_case(seed):
+    """T up to 20000 tokens, E up to 1024, and a threshold regime: per-expert
+    quantiles, a high common threshold (many argmax fallbacks), zero (every
+    pair), or logits placed within a few float steps of each threshold's
+    logit (so the bounds decide nothing and the exact scores do), with NaN
+    and +-inf mixed in."""
+    rng = np.random.default_rng([4096, seed])
+    E = int(rng.choice(R_E_CHOICES))
+    T = int(rng.integers(1, max(2, min(20000, 4_000_000 // E))))
+    mode = str(rng.choice(["quantile", "high", "zero", "edge"]))
+    lg = (rng.standard_normal((T, E)) * rng.choice([0.5, 1.5, 4.0])).astype(np.float32)
+    if mode == "quantile":
+        thr = np.quantile(1 / (1 + np.exp(-lg.astype(np.float64))), rng.uniform(0.5, 0.99), axis=0).astype(np.float32)
+    elif mode == "high":
+        thr = np.full(E, 0.999, np.float32)
+    elif mode == "zero":
+        thr = np.zeros(E, np.float32)
+    else:
+        l0 = (rng.standard_normal(E) * 2).astype(np.float32)
+        thr = (1 / (1 + np.exp(-l0.astype(np.float64)))).astype(np.float32)
+        steps = rng.integers(-6, 7, size=(T, E))
+        lg = np.repeat(l0[None, :], T, 0)
+        for s_ in range(1, 7):
+            up, dn = steps >= s_, steps <= -s_
+            lg[up] = np.nextafter(lg[up], np.float32(np.inf))
+            lg[dn] = np.nextafter(lg[dn], np.float32(-np.inf))
+    lg = np.ascontiguousarray(lg, np.float32)
+    lg[rng.random((T, E)) < 0.003] = np.nan
+    lg[rng.random((T, E)) < 0.002] = np.inf
+    lg[rng.random((T, E)) < 0.002] = -np.inf
+    return T, E, mode, lg, thr
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_routing_and_threshold_update(et, orc, dev, seed):
+    """Routing bit-exact with the oracle on each drawn case, then the EMA
+    update (statistic and thresholds) bit-exact for a drawn k_target."""
+    from test_gpu_parity import assert_route_equal
+
+    T, E, mode, lg, thr = route_case(seed)
+    print(f"route/update case {seed}: T={T} E={E} {mode}", flush=True)
+    L = dev_f32(lg, dev)
+    assert_route_equal(et.route(L, dev_f32(thr, dev)), orc.route(lg, thr))
+    k = int(np.random.default_rng([seed, 9]).integers(1, E + 1))
+    thr0 = np.random.default_rng([seed, 10]).random(E).astype(np.float32)
+    thr_o, stat_o = orc.threshold_update(lg, thr0, k, 0.99)
+    t = dev_f32(thr0, dev)
+    stat = et.threshold_update_(t, L, k, 0.99)
+    np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+    np.testing.assert_array_equal(bits(host(t)), bits(thr_o))
