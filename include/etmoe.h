@@ -204,8 +204,8 @@ int et_dispatch_bwd_router(const void* dxp, const int32_t* token_offsets, const 
                            size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace et_threshold_update needs for T tokens and E experts
- * (it holds the top 16 bits of the T*E score keys, up to T*E candidate keys
- * for the last 14 bits and the radix-select histograms: about 6*T*E bytes). */
+ * (it holds room for T*E candidate keys, of which a selected digit bin's few
+ * are written, and the per-block digit histograms: about 4*T*E bytes). */
 size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 
 /*
@@ -214,7 +214,9 @@ size_t et_threshold_workspace_bytes(int64_t num_tokens, int64_t num_experts);
  *             clamped to [1, T] (NaN scores order as 0)
  *   thr[e]  = fma(momentum, thr[e], (1 - momentum) * stat[e])
  * stat (f32 [E]) may be NULL.  T == 0 leaves thr unchanged.  Exact selection
- * (radix select on the score bits), so thr is bit-exact with the definition.
+ * (a histogram of the scores' digits floor(score * 256), then a radix select
+ * over the score bits of the selected digit's keys), so thr is bit-exact with
+ * the definition.
  * Implements the EMA threshold update of the path (no reference counterpart).
  */
 int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int64_t num_experts,
