@@ -386,20 +386,30 @@ def test_threshold_update_ties(et, orc, dev, T, E, k):
     stat = et.threshold_update_(thr, dev_f32(lg, dev), k, 0.9)
     np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
     np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
+    # the same through route_update
+    thr = dev_f32(thr0, dev)
+    stat = torch.empty(E, device=dev)
+    et.route_update(dev_f32(lg, dev), thr, k, 0.9, stat=stat)
+    np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+    np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
 
 
-def test_threshold_update_logits_at_digit_edges(et, orc, dev):
+@pytest.mark.parametrize("entry", ["threshold_update", "route_update"])
+def test_threshold_update_logits_at_digit_edges(et, orc, dev, entry):
     """The histogram pass takes each score's digit floor(score * 256) from a
     fast sigmoid checked against logit bounds of the digit edges b / 256, and
     the collect pass skips logits outside the chosen digit's bounds; only
     logits near an edge take the exact score.  Here most logits sit within
     40 float steps of the logit of an edge (a different edge per column, and
     in the last columns many columns' statistic falls inside such a crowd),
-    with NaN and +-inf mixed in: statistic and thresholds bit-exact."""
+    with NaN and +-inf mixed in: statistic and thresholds bit-exact, through
+    threshold_update_ and through route_update."""
+    print(f"digit edges via {entry}", flush=True)
+    bins = 256
     T, E, k = 8192, 64, 8
     rng = np.random.default_rng(31)
-    edges = rng.integers(1, 256, size=E)
-    l0 = np.log(edges / 256.0) - np.log1p(-edges / 256.0)          # logit of b / 256
+    edges = rng.integers(1, bins, size=E)
+    l0 = np.log(edges / bins) - np.log1p(-edges / bins)          # logit of b / bins
     l0 = l0.astype(np.float32)
     target = np.repeat(l0[None, :], T, 0)
     steps = rng.integers(-40, 41, size=(T, E))
@@ -419,11 +429,16 @@ def test_threshold_update_logits_at_digit_edges(et, orc, dev):
     thr0 = rng.random(E).astype(np.float32)
     thr_o, stat_o = orc.threshold_update(lg, thr0, k, 0.99)
     thr = dev_f32(thr0, dev)
-    stat = et.threshold_update_(thr, dev_f32(lg, dev), k, 0.99)
+    L = dev_f32(lg, dev)
+    if entry == "threshold_update":
+        stat = et.threshold_update_(thr, L, k, 0.99)
+    else:
+        stat = torch.empty(E, device=dev)
+        assert_route_equal(et.route_update(L, thr, k, 0.99, stat=stat), orc.route(lg, thr0))
     np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
     np.testing.assert_array_equal(bits(host(thr)), bits(thr_o))
     # the statistic of most columns lies in the crowd at the edge
-    at_edge = np.abs(stat_o - edges / 256.0) < 1e-4
+    at_edge = np.abs(stat_o - edges / bins) < 1e-4
     assert at_edge.sum() >= E // 4
 
 
@@ -440,7 +455,8 @@ def _plans_identical(a, b):
 
 
 @pytest.mark.parametrize("T,E,k,cap", [(8192, 64, 8, None), (1, 4, 2, None), (5000, 128, 8, "under"),
-                                       (131072, 64, 8, "exact"), (300, 1024, 16, None), (999, 7, 3, None)])
+                                       (131072, 64, 8, "exact"), (300, 1024, 16, None), (999, 7, 3, None),
+                                       (20000, 256, 8, None), (3, 65, 2, None), (4097, 200, 5, None)])
 def test_route_update_matches_route_then_update(et, orc, dev, T, E, k, cap):
     """et_route_update equals route followed by threshold_update_ bit for
     bit, and the oracle."""

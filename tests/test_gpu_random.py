@@ -177,7 +177,8 @@ def route_case(seed):
 @pytest.mark.parametrize("seed", range(40))
 def test_random_routing_and_threshold_update(et, orc, dev, seed):
     """Routing bit-exact with the oracle on each drawn case, then the EMA
-    update (statistic and thresholds) bit-exact for a drawn k_target."""
+    update (statistic and thresholds) bit-exact for a drawn k_target, alone
+    and in route_update."""
     from test_gpu_parity import assert_route_equal
 
     T, E, mode, lg, thr = route_case(seed)
@@ -191,3 +192,12 @@ def test_random_routing_and_threshold_update(et, orc, dev, seed):
     stat = et.threshold_update_(t, L, k, 0.99)
     np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
     np.testing.assert_array_equal(bits(host(t)), bits(thr_o))
+    # route_update: routes with thr, then updates it (E <= 256 takes the
+    # digit histograms from the routing pass)
+    thr_o2, stat_o2 = orc.threshold_update(lg, thr, k, 0.99)
+    t2 = dev_f32(thr, dev)
+    stat2 = torch.empty(E, device=dev)
+    plan = et.route_update(L, t2, k, 0.99, stat=stat2)
+    assert_route_equal(plan, orc.route(lg, thr))
+    np.testing.assert_array_equal(bits(host(stat2)), bits(stat_o2))
+    np.testing.assert_array_equal(bits(host(t2)), bits(thr_o2))
