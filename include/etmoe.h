@@ -80,7 +80,10 @@ const char* et_last_error(void);
 
 /* Bytes of device workspace et_route needs for T tokens and E experts: the
  * routed pairs of every 8-token group (8 * E entries of 8 bytes reserved per
- * group, about 8 * T * E bytes in all) plus per-group and per-tile counts. */
+ * group, about 8 * T * E bytes in all) plus per-group and per-tile counts.
+ * Where that would pass 1 GiB (T * E above about 134 M), et_route runs the
+ * two-read kernels instead (same outputs), and this is their workspace: per-
+ * block counts, a few MB. */
 size_t et_route_workspace_bytes(int64_t num_tokens, int64_t num_experts);
 
 /*
@@ -114,11 +117,11 @@ int et_route(const float* logits, const float* thr, int64_t num_tokens, int64_t 
  * callers that cannot allocate: code under HIP graph capture, serving loops
  * and harnesses that forbid hipMalloc.  Arguments and outputs are those of
  * et_route (bit-identical results); the call runs on the current device, whose
- * scratch address it looks up once (on its first call there).  Sizes whose
- * et_route_workspace_bytes(T, E) exceeds the scratch are rejected with
- * ET_ERR_WORKSPACE_TOO_SMALL: every T fits for E <= 408.  It runs the two-read
- * routing kernels (a count pass and a fill pass that both read the logits),
- * whose workspace is O(E) per block, not et_route's pair lists.  All calls on
+ * scratch address it looks up once (on its first call there).  It runs the
+ * two-read routing kernels (a count pass and a fill pass that both read the
+ * logits), whose workspace is O(E) per block, not et_route's pair lists; sizes
+ * whose two-read workspace exceeds the scratch are rejected with
+ * ET_ERR_WORKSPACE_TOO_SMALL (every T fits for E <= 408).  All calls on
  * one GPU share the scratch: calls that overlap in time on one GPU (different
  * streams or host threads) race.
  * No counterpart in the reference: an extra entry point of this library.
