@@ -229,8 +229,10 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
 /*
  * Routing and the EMA threshold update of one training batch in one call:
  * the results of et_route (with the thresholds from before the update)
- * followed by et_threshold_update, bit for bit.  It enqueues exactly those
- * two calls' kernels on `stream`, in that order.
+ * followed by et_threshold_update, bit for bit, with every kernel on
+ * `stream`.  Where et_route takes its pair lists, the two calls' launches
+ * interleave (count, histogram, scan together with the bin select, place,
+ * collect, final select): one launch fewer than the two calls.
  * Workspaces: route_workspace as et_route's, thr_workspace as
  * et_threshold_update's; their byte ranges must not overlap
  * (ET_ERR_INVALID_ARGUMENT).

@@ -25,6 +25,7 @@
 
 #include "et_common.hpp"
 #include "et_route_internal.hpp"
+#include "et_threshold_internal.hpp"
 
 namespace et {
 
@@ -821,20 +822,20 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave, GM <= 2 ? 8 : 1) void route_pa
 // totals of the earlier segments.
 constexpr int kSegTiles = 256;
 
-__global__ __launch_bounds__(kScanThreads) void route_segscan_kernel(
-    const int32_t* __restrict__ block_counts, const int32_t* __restrict__ block_slots, int NB, int E, int RS,
-    int32_t* __restrict__ block_base, int32_t* __restrict__ seg_counts, int32_t* __restrict__ block_slot_base,
-    int32_t* __restrict__ seg_slots)
+// Block (seg, gy) of the scan, kScanThreads threads.
+__device__ __forceinline__ void route_segscan_block(
+    int seg, int gy, const int32_t* __restrict__ block_counts, const int32_t* __restrict__ block_slots, int NB,
+    int E, int RS, int32_t* __restrict__ block_base, int32_t* __restrict__ seg_counts,
+    int32_t* __restrict__ block_slot_base, int32_t* __restrict__ seg_slots)
 {
     __shared__ int part[kScanWaves][kWave];
     __shared__ int wtot[kScanWaves];
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
     const int G = (E + kWave - 1) / kWave;
-    const int seg = (int)blockIdx.x;
     const int s0 = seg * RS, s1 = min(NB, s0 + RS);
-    if ((int)blockIdx.y < G) {
-        const int e = (int)blockIdx.y * kWave + lane;
+    if (gy < G) {
+        const int e = gy * kWave + lane;
         const bool ve = e < E;
         const int ec = min(e, E - 1);
         const int RW = (RS + kScanWaves - 1) / kScanWaves;
@@ -878,6 +879,37 @@ __global__ __launch_bounds__(kScanThreads) void route_segscan_kernel(
         if (r < s1) block_slot_base[r] = run;
         if (tid == 0) seg_slots[seg] = total;
     }
+}
+
+__global__ __launch_bounds__(kScanThreads) void route_segscan_kernel(
+    const int32_t* __restrict__ block_counts, const int32_t* __restrict__ block_slots, int NB, int E, int RS,
+    int32_t* __restrict__ block_base, int32_t* __restrict__ seg_counts, int32_t* __restrict__ block_slot_base,
+    int32_t* __restrict__ seg_slots)
+{
+    route_segscan_block((int)blockIdx.x, (int)blockIdx.y, block_counts, block_slots, NB, E, RS, block_base,
+                        seg_counts, block_slot_base, seg_slots);
+}
+
+// et_route_update's scan launch: blocks [0, E) run the EMA update's bin
+// select (one expert each), blocks E + seg * (G + 1) + gy the segmented scan.
+// Both only read what the count and histogram passes wrote, and each role
+// fills a 1024-thread block.
+static_assert(kScanThreads == kSelectThreads, "the scan and bin-select blocks have one size");
+
+__global__ __launch_bounds__(kScanThreads) void upd_scan_bin_kernel(
+    int E, int nbx, const uint32_t* __restrict__ partial, uint32_t c, uint32_t* __restrict__ bin,
+    uint32_t* __restrict__ rank, float* __restrict__ bnd, const int32_t* __restrict__ block_counts,
+    const int32_t* __restrict__ block_slots, int NB, int RS, int32_t* __restrict__ block_base,
+    int32_t* __restrict__ seg_counts, int32_t* __restrict__ block_slot_base, int32_t* __restrict__ seg_slots)
+{
+    const int b = (int)blockIdx.x;
+    if (b < E) {
+        thr_bin_block(b, nbx, partial, c, bin, rank, bnd);
+        return;
+    }
+    const int G1 = (E + kWave - 1) / kWave + 1;
+    route_segscan_block((b - E) / G1, (b - E) % G1, block_counts, block_slots, NB, E, RS, block_base, seg_counts,
+                        block_slot_base, seg_slots);
 }
 
 // Place kernel: block b = tile b; wave i handles the tile's route groups
@@ -1209,11 +1241,9 @@ static PairWs pair_ws_layout(void* base, const PairPlan& p, int64_t T, int64_t E
     return ws;
 }
 
-// The three launches of et_route on stream s (arguments checked).
-static int route_pairs_path(const float* logits, const float* thr, int64_t T, int64_t E, int32_t* counts,
-                            int32_t* expert_offsets, int32_t* token_offsets, int32_t* sorted_token,
-                            float* slot_gate, int32_t* token_slot, int64_t slot_capacity, const PairPlan& p,
-                            const PairWs& ws, hipStream_t s)
+// The count pass of the pair-list path on stream s.
+static int pairs_count(const float* logits, const float* thr, int64_t T, int64_t E, const PairPlan& p,
+                       const PairWs& ws, hipStream_t s)
 {
     const int Ti = (int)T, Ei = (int)E, gpt = (int)p.gpt, NB = (int)p.ntiles;
     ET_SWITCH_GROUPS(p.G, {
@@ -1224,11 +1254,16 @@ static int route_pairs_path(const float* logits, const float* thr, int64_t T, in
             logits, thr, Ti, Ei, gpt, ws.pairs, ws.group_counts, ws.group_slots, ws.block_counts,
             ws.block_slots);
     });
-    if (int rc = check_launch("route_pairs_kernel")) return rc;
+    return check_launch("route_pairs_kernel");
+}
+
+// The place pass of the pair-list path on stream s.
+static int pairs_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                       int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
+                       const PairPlan& p, const PairWs& ws, hipStream_t s)
+{
+    const int Ti = (int)T, Ei = (int)E, gpt = (int)p.gpt, NB = (int)p.ntiles;
     const int S = (int)p.nseg, RS = (int)p.seg_tiles;
-    route_segscan_kernel<<<dim3(S, p.G + 1), dim3(kScanThreads), 0, s>>>(
-        ws.block_counts, ws.block_slots, NB, Ei, RS, ws.block_base, ws.seg_counts, ws.block_slot_base, ws.seg_slots);
-    if (int rc = check_launch("route_segscan_kernel")) return rc;
     ET_SWITCH_GROUPS(p.G, {
         const int PG = gpt >= kPlaceGroups ? kPlaceGroups : 1;
         const int nwave = gpt / PG;
@@ -1239,6 +1274,50 @@ static int route_pairs_path(const float* logits, const float* thr, int64_t T, in
             token_offsets, sorted_token, slot_gate, token_slot, slot_capacity);
     });
     return check_launch("route_place_kernel");
+}
+
+// The three launches of et_route on stream s (arguments checked).
+static int route_pairs_path(const float* logits, const float* thr, int64_t T, int64_t E, int32_t* counts,
+                            int32_t* expert_offsets, int32_t* token_offsets, int32_t* sorted_token,
+                            float* slot_gate, int32_t* token_slot, int64_t slot_capacity, const PairPlan& p,
+                            const PairWs& ws, hipStream_t s)
+{
+    if (int rc = pairs_count(logits, thr, T, E, p, ws, s)) return rc;
+    const int S = (int)p.nseg, RS = (int)p.seg_tiles;
+    route_segscan_kernel<<<dim3(S, p.G + 1), dim3(kScanThreads), 0, s>>>(
+        ws.block_counts, ws.block_slots, (int)p.ntiles, (int)E, RS, ws.block_base, ws.seg_counts,
+        ws.block_slot_base, ws.seg_slots);
+    if (int rc = check_launch("route_segscan_kernel")) return rc;
+    return pairs_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
+                       slot_capacity, p, ws, s);
+}
+
+int route_update_count(const float* logits, const float* thr, int64_t T, int64_t E, void* workspace,
+                       hipStream_t s)
+{
+    const PairPlan p = pair_plan(T, E);
+    return pairs_count(logits, thr, T, E, p, pair_ws_layout(workspace, p, T, E), s);
+}
+
+int route_update_scan_bin(int64_t T, int64_t E, void* workspace, const uint32_t* partial, int nbx, uint32_t c,
+                          uint32_t* bin, uint32_t* rank, float* bnd, hipStream_t s)
+{
+    const PairPlan p = pair_plan(T, E);
+    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    const int S = (int)p.nseg, RS = (int)p.seg_tiles;
+    upd_scan_bin_kernel<<<dim3((unsigned)(E + S * (p.G + 1))), dim3(kScanThreads), 0, s>>>(
+        (int)E, nbx, partial, c, bin, rank, bnd, ws.block_counts, ws.block_slots, (int)p.ntiles, RS, ws.block_base,
+        ws.seg_counts, ws.block_slot_base, ws.seg_slots);
+    return check_launch("upd_scan_bin_kernel");
+}
+
+int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                       int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
+                       void* workspace, hipStream_t s)
+{
+    const PairPlan p = pair_plan(T, E);
+    return pairs_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
+                       slot_capacity, p, pair_ws_layout(workspace, p, T, E), s);
 }
 
 }  // namespace et
@@ -1253,6 +1332,8 @@ constexpr size_t kPairWsLimit = size_t(1) << 30;
 static size_t pair_ws_bytes(int64_t T, int64_t E) { return pair_ws_layout(nullptr, pair_plan(T, E), T, E).bytes; }
 static size_t two_read_ws_bytes(int64_t T, int64_t E) { return route_ws_layout(nullptr, route_plan(T, E), E).bytes; }
 static bool use_pairs(int64_t T, int64_t E) { return pair_ws_bytes(T, E) <= kPairWsLimit; }
+
+bool et::route_uses_pairs(int64_t T, int64_t E) { return T > 0 && E >= 1 && use_pairs(T, E); }
 
 static int route_two_read(const float* logits, const float* thr, int64_t T, int64_t E, int32_t* counts,
                           int32_t* expert_offsets, int32_t* token_offsets, int32_t* sorted_token, float* slot_gate,

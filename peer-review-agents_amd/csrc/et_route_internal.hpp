@@ -138,6 +138,10 @@ int route_check(const char* fn, const float* logits, const float* thr, int64_t T
                 const int32_t* sorted_token, const float* slot_gate, const int32_t* token_slot,
                 int64_t slot_capacity);
 
+// et_route takes the pair-list path on (T, E) (T > 0): its pair lists fit
+// the 1 GiB bound; otherwise the two-read kernels.
+bool route_uses_pairs(int64_t T, int64_t E);
+
 // Column-wise exclusive scan of the per-block expert counts (NB rows of E)
 // into counts[E] and block_base[NB * E], and of the per-block slot totals
 // into block_slot_base[NB].

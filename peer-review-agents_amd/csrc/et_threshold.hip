@@ -36,25 +36,11 @@
 
 #include "et_common.hpp"
 #include "et_route_internal.hpp"
+#include "et_threshold_internal.hpp"
 
 namespace et {
 
 static inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
-
-constexpr int kDigitBits = 8;
-constexpr int kBins = 1 << kDigitBits;      // histogram digits: floor(score * kBins)
-constexpr int kBinWords = kBins / 2;        // two 16-bit counts to a word
-constexpr int kHistWaves = 16;
-constexpr int kHistThreads = kHistWaves * kWave;
-constexpr int64_t kHistBlocks = 256;        // blocks of a pass (whole grid)
-constexpr int kHistUT = 16;                 // tokens in flight per wave
-constexpr int64_t kMaxTokensPerBlock = 65535;  // LDS counts are 16-bit
-constexpr int kPitch = kWave + 1;           // LDS words per digit pair (padded)
-constexpr int kHistWords = kWave * kBinWords;  // words of one block histogram
-constexpr int kSelectThreads = 1024;
-constexpr int kSelectSplit = kSelectThreads / kBinWords;   // bin-select threads per word
-constexpr int kSelectRound = 8;             // partial-histogram loads in flight per select thread
-constexpr int kFinalLdsKeys = 12288;        // candidates the final select holds in LDS (48 KiB)
 
 // Token blocks per 64-expert group of the histogram and collect passes.
 struct HistGrid {
@@ -109,23 +95,6 @@ static ThrWs thr_ws_layout(void* base, int64_t T, int64_t E)
     ws.bytes = off;
     return ws;
 }
-
-// The key of a logit: the bits of its score, NaN as 0 (at most f2u(1.0)).
-__device__ __forceinline__ uint32_t score_key(float l)
-{
-    const float sc = sigmoid(l);
-    return (sc != sc) ? 0u : f2u(sc);
-}
-
-// The histogram digit of a key: floor(score * kBins), kBins - 1 for a score
-// of 1.  (score * kBins is exact, and the conversion truncates.)
-__device__ __forceinline__ uint32_t score_digit(uint32_t key)
-{
-    return min((uint32_t)(u2f(key) * (float)kBins), (uint32_t)kBins - 1u);
-}
-
-// The score at the lower edge of digit bin b, b / kBins (exact).
-__device__ __forceinline__ float bin_edge(uint32_t b) { return (float)b * (1.0f / (float)kBins); }
 
 // LDS histogram of one block: 16-bit counts, two digits to a word, word
 // (d >> 1) * kPitch + lane; a block covers at most 65535 tokens, so a half
@@ -255,91 +224,13 @@ __global__ __launch_bounds__(kHistThreads) void thr_collect_kernel(
     if (tid < kWave && ve) cand_n[(int64_t)e * gridDim.x + blockIdx.x] = cn[tid];
 }
 
-// Wave 0 of a select block: the bin of the rank-th largest key (rank r >= 1)
-// given NB bin counts cnt(bin) (NB = 64, 128 or 256), bins walked from the
-// top.  The lane that holds it returns true with the bin and the rank left
-// inside the bin.
-template <int NB, typename F>
-__device__ __forceinline__ bool find_digit(F cnt, int r, uint32_t& bin, int& rank_in)
-{
-    constexpr int PER = NB / kWave;
-    const int lane = lane_id();
-    // position p = PER*lane + i walks the bins from the top: bin = NB - 1 - p
-    uint32_t c[PER];
-    int tot = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        c[i] = cnt(NB - 1 - (PER * lane + i));
-        tot += (int)c[i];
-    }
-    const int incl = wave_incl_scan(tot);
-    const int excl = incl - tot;
-    if (!(excl < r && r <= incl)) return false;
-    int run = excl;
-    int pos = PER * lane + PER - 1;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        if (run + (int)c[i] >= r) { pos = PER * lane + i; break; }
-        run += (int)c[i];
-    }
-    bin = (uint32_t)(NB - 1 - pos);
-    rank_in = r - run;
-    return true;
-}
-
-// Bin select, one block per expert: counts[d] = the sum of the expert's block
-// histograms (kSelectSplit threads per word of two digits, each over every
-// kSelectSplit-th block, all loads of a round issued together; the two 16-bit
-// halves are added separately), then wave 0 finds the digit bin that holds the
-// c-th largest key, and the logit bounds of the bin's scores [b / kBins,
-// (b + 1) / kBins).
+// The bin select's own kernel (thr_bin_block: et_threshold_internal.hpp).
 __global__ __launch_bounds__(kSelectThreads) void thr_bin_kernel(int E, int nblocks,
                                                                  const uint32_t* __restrict__ partial, uint32_t c,
                                                                  uint32_t* __restrict__ bin,
                                                                  uint32_t* __restrict__ rank, float* __restrict__ bnd)
 {
-    __shared__ uint32_t part[kSelectSplit][kBins];
-    const int e = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int q = tid / kBinWords, j = tid % kBinWords;
-    const uint32_t* src = partial + (int64_t)(e >> 6) * nblocks * kHistWords + (e & 63) * kBinWords + j;
-    uint32_t lo = 0u, hi = 0u;
-    for (int b0 = q; b0 < nblocks; b0 += kSelectRound * kSelectSplit) {
-        uint32_t v[kSelectRound];
-#pragma unroll
-        for (int i = 0; i < kSelectRound; ++i)
-            v[i] = src[(int64_t)min(b0 + i * kSelectSplit, nblocks - 1) * kHistWords];
-#pragma unroll
-        for (int i = 0; i < kSelectRound; ++i) {
-            const uint32_t w = (b0 + i * kSelectSplit < nblocks) ? v[i] : 0u;
-            lo += w & 0xffffu;
-            hi += w >> 16;
-        }
-    }
-    part[q][2 * j] = lo;
-    part[q][2 * j + 1] = hi;
-    __syncthreads();
-    if (tid >= kWave) return;
-    auto pass_count = [&](int b) {
-        uint32_t n = 0u;
-#pragma unroll
-        for (int k = 0; k < kSelectSplit; ++k) n += part[k][b];
-        return n;
-    };
-    uint32_t b;
-    int rin;
-    if (find_digit<kBins>(pass_count, (int)c, b, rin)) {
-        bin[e] = b;
-        rank[e] = (uint32_t)rin;
-        // a logit at or below lo_a scores below bin_edge(b); one at or above
-        // hi_b scores at least bin_edge(b + 1) (nothing is above the last
-        // bin, and a NaN bound decides nothing: comparisons with it are false)
-        float hi_a, lo_a, hi_b, lo_b;
-        select_bounds(bin_edge(b), hi_a, lo_a);
-        select_bounds(bin_edge(b + 1u), hi_b, lo_b);
-        bnd[2 * e] = lo_a;
-        bnd[2 * e + 1] = b == (uint32_t)kBins - 1u ? __builtin_nanf("") : hi_b;
-    }
+    thr_bin_block((int)blockIdx.x, nblocks, partial, c, bin, rank, bnd);
 }
 
 // Final select, one block per expert: the rank-th largest listed key.  The
@@ -456,9 +347,7 @@ __global__ __launch_bounds__(kSelectThreads) void thr_final_kernel(
 static int thr_passes(const float* logits, int64_t T, int64_t E, int64_t k_target, float* thr, float* stat,
                       float momentum, const ThrWs& ws, hipStream_t s)
 {
-    int64_t c = (T * k_target + E - 1) / E;
-    if (c < 1) c = 1;
-    if (c > T) c = T;
+    const int64_t c = thr_rank(T, E, k_target);
     const int Ti = (int)T, Ei = (int)E;
     const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
     const dim3 grid((unsigned)ws.g.blocks, groups);
@@ -542,11 +431,35 @@ extern "C" int et_route_update(const float* logits, float* thr, int64_t T, int64
     if (int rc = thr_check(fn, logits, thr, T, E, k_target, momentum, thr_workspace, thr_workspace_bytes)) return rc;
     if (overlaps(route_workspace, rneed, thr_workspace, thr_ws_layout(nullptr, T, E).bytes))
         return fail(ET_ERR_INVALID_ARGUMENT, "et_route_update: the route and threshold workspaces overlap");
-    // the routing reads thr before the update writes it: both on `stream`
+    // The routing reads thr before the update writes it: both on `stream`.
+    // On the pair-list path the routing's launches and the update's passes
+    // interleave, with the update's bin select in the routing scan's launch:
+    // count, histogram, scan + bin select, place, collect, final select.
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const ThrWs ws = thr_ws_layout(thr_workspace, T, E);
+    if (T > 0 && route_uses_pairs(T, E)) {
+        const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
+        const dim3 grid((unsigned)ws.g.blocks, groups);
+        const int Ti = (int)T, Ei = (int)E, tpb = (int)ws.g.tpb, nb = (int)ws.g.blocks;
+        if (int rc = route_update_count(logits, thr, T, E, route_workspace, s)) return rc;
+        thr_hist_kernel<kHistUT><<<grid, dim3(kHistThreads), 0, s>>>(logits, Ti, Ei, tpb, ws.partial);
+        if (int rc = check_launch("thr_hist_kernel")) return rc;
+        if (int rc = route_update_scan_bin(T, E, route_workspace, ws.partial, nb,
+                                           (uint32_t)thr_rank(T, E, k_target), ws.bin, ws.rank, ws.bnd, s))
+            return rc;
+        if (int rc = route_update_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
+                                        token_slot, slot_capacity, route_workspace, s))
+            return rc;
+        thr_collect_kernel<kHistUT><<<grid, dim3(kHistThreads), 0, s>>>(logits, Ti, Ei, tpb, ws.bin, ws.bnd,
+                                                                         ws.cand, ws.cand_n);
+        if (int rc = check_launch("thr_collect_kernel")) return rc;
+        thr_final_kernel<<<dim3((unsigned)Ei), dim3(kSelectThreads), 0, s>>>(Ei, nb, Ti, tpb, ws.bin, ws.rank, ws.key,
+                                                                            ws.cand, ws.cand_n, thr, stat, momentum);
+        return check_launch("thr_final_kernel");
+    }
     if (int rc = et_route(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                           token_slot, slot_capacity, route_workspace, route_workspace_bytes, stream))
         return rc;
     if (T == 0) return ET_OK;
-    return thr_passes(logits, T, E, k_target, thr, stat, momentum, thr_ws_layout(thr_workspace, T, E),
-                      static_cast<hipStream_t>(stream));
+    return thr_passes(logits, T, E, k_target, thr, stat, momentum, ws, s);
 }

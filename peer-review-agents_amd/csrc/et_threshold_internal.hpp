@@ -1,0 +1,157 @@
+// et_threshold_internal.hpp -- what the EMA threshold update shares with the
+// routing file: its digit constants and score keys, its bin select as a
+// per-block device function (run by its own kernel in et_threshold.hip and,
+// for et_route_update, beside the routing's segmented scan in et_route.hip),
+// and the routing launches that et_route_update interleaves with the
+// update's passes.  Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "et_common.hpp"
+#include "et_route_internal.hpp"
+
+namespace et {
+
+constexpr int kDigitBits = 8;
+constexpr int kBins = 1 << kDigitBits;      // histogram digits: floor(score * kBins)
+constexpr int kBinWords = kBins / 2;        // two 16-bit counts to a word
+constexpr int kHistWaves = 16;
+constexpr int kHistThreads = kHistWaves * kWave;
+constexpr int64_t kHistBlocks = 256;        // blocks of a pass (whole grid)
+constexpr int kHistUT = 16;                 // tokens in flight per wave
+constexpr int64_t kMaxTokensPerBlock = 65535;  // LDS counts are 16-bit
+constexpr int kPitch = kWave + 1;           // LDS words per digit pair (padded)
+constexpr int kHistWords = kWave * kBinWords;  // words of one block histogram
+constexpr int kSelectThreads = 1024;
+constexpr int kSelectSplit = kSelectThreads / kBinWords;   // bin-select threads per word
+constexpr int kSelectRound = 8;             // partial-histogram loads in flight per select thread
+constexpr int kFinalLdsKeys = 12288;        // candidates the final select holds in LDS (48 KiB)
+
+// The key of a logit: the bits of its score, NaN as 0 (at most f2u(1.0)).
+__device__ __forceinline__ uint32_t score_key(float l)
+{
+    const float sc = sigmoid(l);
+    return (sc != sc) ? 0u : f2u(sc);
+}
+
+// The histogram digit of a key: floor(score * kBins), kBins - 1 for a score
+// of 1.  (score * kBins is exact, and the conversion truncates.)
+__device__ __forceinline__ uint32_t score_digit(uint32_t key)
+{
+    return min((uint32_t)(u2f(key) * (float)kBins), (uint32_t)kBins - 1u);
+}
+
+// The score at the lower edge of digit bin b, b / kBins (exact).
+__device__ __forceinline__ float bin_edge(uint32_t b) { return (float)b * (1.0f / (float)kBins); }
+
+// Wave 0 of a select block: the bin of the rank-th largest key (rank r >= 1)
+// given NB bin counts cnt(bin) (NB = 64, 128 or 256), bins walked from the
+// top.  The lane that holds it returns true with the bin and the rank left
+// inside the bin.
+template <int NB, typename F>
+__device__ __forceinline__ bool find_digit(F cnt, int r, uint32_t& bin, int& rank_in)
+{
+    constexpr int PER = NB / kWave;
+    const int lane = lane_id();
+    // position p = PER*lane + i walks the bins from the top: bin = NB - 1 - p
+    uint32_t c[PER];
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        c[i] = cnt(NB - 1 - (PER * lane + i));
+        tot += (int)c[i];
+    }
+    const int incl = wave_incl_scan(tot);
+    const int excl = incl - tot;
+    if (!(excl < r && r <= incl)) return false;
+    int run = excl;
+    int pos = PER * lane + PER - 1;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        if (run + (int)c[i] >= r) { pos = PER * lane + i; break; }
+        run += (int)c[i];
+    }
+    bin = (uint32_t)(NB - 1 - pos);
+    rank_in = r - run;
+    return true;
+}
+
+// Bin select, one block per expert: counts[d] = the sum of the expert's block
+// histograms (kSelectSplit threads per word of two digits, each over every
+// kSelectSplit-th block, all loads of a round issued together; the two 16-bit
+// halves are added separately), then wave 0 finds the digit bin that holds the
+// c-th largest key, and the logit bounds of the bin's scores [b / kBins,
+// (b + 1) / kBins).
+// Block e (kSelectThreads threads) of the bin select.
+__device__ __forceinline__ void thr_bin_block(int e, int nblocks, const uint32_t* __restrict__ partial, uint32_t c,
+                                              uint32_t* __restrict__ bin, uint32_t* __restrict__ rank,
+                                              float* __restrict__ bnd)
+{
+    __shared__ uint32_t part[kSelectSplit][kBins];
+    const int tid = threadIdx.x;
+    const int q = tid / kBinWords, j = tid % kBinWords;
+    const uint32_t* src = partial + (int64_t)(e >> 6) * nblocks * kHistWords + (e & 63) * kBinWords + j;
+    uint32_t lo = 0u, hi = 0u;
+    for (int b0 = q; b0 < nblocks; b0 += kSelectRound * kSelectSplit) {
+        uint32_t v[kSelectRound];
+#pragma unroll
+        for (int i = 0; i < kSelectRound; ++i)
+            v[i] = src[(int64_t)min(b0 + i * kSelectSplit, nblocks - 1) * kHistWords];
+#pragma unroll
+        for (int i = 0; i < kSelectRound; ++i) {
+            const uint32_t w = (b0 + i * kSelectSplit < nblocks) ? v[i] : 0u;
+            lo += w & 0xffffu;
+            hi += w >> 16;
+        }
+    }
+    part[q][2 * j] = lo;
+    part[q][2 * j + 1] = hi;
+    __syncthreads();
+    if (tid >= kWave) return;
+    auto pass_count = [&](int b) {
+        uint32_t n = 0u;
+#pragma unroll
+        for (int k = 0; k < kSelectSplit; ++k) n += part[k][b];
+        return n;
+    };
+    uint32_t b;
+    int rin;
+    if (find_digit<kBins>(pass_count, (int)c, b, rin)) {
+        bin[e] = b;
+        rank[e] = (uint32_t)rin;
+        // a logit at or below lo_a scores below bin_edge(b); one at or above
+        // hi_b scores at least bin_edge(b + 1) (nothing is above the last
+        // bin, and a NaN bound decides nothing: comparisons with it are false)
+        float hi_a, lo_a, hi_b, lo_b;
+        select_bounds(bin_edge(b), hi_a, lo_a);
+        select_bounds(bin_edge(b + 1u), hi_b, lo_b);
+        bnd[2 * e] = lo_a;
+        bnd[2 * e + 1] = b == (uint32_t)kBins - 1u ? __builtin_nanf("") : hi_b;
+    }
+}
+
+// The rank of the statistic: c = ceil(T * k_target / E), within [1, T].
+inline int64_t thr_rank(int64_t T, int64_t E, int64_t k_target)
+{
+    int64_t c = (T * k_target + E - 1) / E;
+    if (c < 1) c = 1;
+    if (c > T) c = T;
+    return c;
+}
+
+// et_route's three launches on the pair-list path (route_uses_pairs(T, E),
+// arguments and workspace already checked, T > 0), for et_route_update, which
+// puts the EMA update's histogram pass between the count and the scan, and
+// runs the update's bin select (over nbx histogram blocks per 64-expert
+// group, statistic rank c) in the scan's launch.
+int route_update_count(const float* logits, const float* thr, int64_t T, int64_t E, void* workspace,
+                       hipStream_t s);
+int route_update_scan_bin(int64_t T, int64_t E, void* workspace, const uint32_t* partial, int nbx, uint32_t c,
+                          uint32_t* bin, uint32_t* rank, float* bnd, hipStream_t s);
+int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
+                       int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
+                       void* workspace, hipStream_t s);
+
+}  // namespace et

@@ -630,8 +630,9 @@ def route_update(logits: torch.Tensor, thr: torch.Tensor, k_target: int, momentu
                  thr_workspace: Optional[torch.Tensor] = None) -> RoutingPlan:
     """Routing with the current thresholds, then the EMA update of thr from
     the same batch, in one call: the same results as :func:`route` followed by
-    :func:`threshold_update_` (et_route_update), whose kernels it enqueues on
-    the current stream in that order."""
+    :func:`threshold_update_` (et_route_update), with every kernel on the
+    current stream and the routing scan and the update's bin select in one
+    launch."""
     _require(logits, "logits", torch.float32, 2)
     dev = logits.device
     T, E = logits.shape
