@@ -821,7 +821,9 @@ def combine_autograd(yp: torch.Tensor, logits: torch.Tensor, plan: RoutingPlan) 
 class ExpertThresholdRouter(torch.nn.Module):
     """Per-expert thresholds with the EMA update applied after each training
     batch (route with the current thresholds, then update them from the batch),
-    the way batch statistics are kept in a running buffer."""
+    the way batch statistics are kept in a running buffer.  In training mode
+    both go through :func:`route_update` (one call, the same bits as
+    :func:`route` then :func:`threshold_update_`); in eval mode it only routes."""
 
     def __init__(self, num_experts: int, k_target: int, momentum: float = 0.99,
                  init_threshold: float = 0.5, device=None):
@@ -834,7 +836,7 @@ class ExpertThresholdRouter(torch.nn.Module):
                                                dtype=torch.float32, device=device))
 
     def forward(self, logits: torch.Tensor, *, slot_capacity: Optional[int] = None) -> RoutingPlan:
-        plan = route(logits.detach(), self.thr, slot_capacity=slot_capacity)
         if self.training:
-            threshold_update_(self.thr, logits.detach(), self.k_target, self.momentum)
-        return plan
+            return route_update(logits.detach(), self.thr, self.k_target, self.momentum,
+                                slot_capacity=slot_capacity)
+        return route(logits.detach(), self.thr, slot_capacity=slot_capacity)
