@@ -230,9 +230,10 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
  * Routing and the EMA threshold update of one training batch in one call:
  * the results of et_route (with the thresholds from before the update)
  * followed by et_threshold_update, bit for bit, with every kernel on
- * `stream`.  Where et_route takes its pair lists, the two calls' launches
- * interleave (count, histogram, scan together with the bin select, place,
- * collect, final select): one launch fewer than the two calls.
+ * `stream`.  Where et_route takes its pair lists (up to 256 experts), the
+ * update's small passes run in the routing's launches (histogram; count with
+ * the bin select; scan with the collect pass; place; final select): five
+ * launches for the two calls' seven.
  * Workspaces: route_workspace as et_route's, thr_workspace as
  * et_threshold_update's; their byte ranges must not overlap
  * (ET_ERR_INVALID_ARGUMENT).

@@ -713,14 +713,37 @@ __device__ __forceinline__ bool route_walk(const float* __restrict__ logits, int
     return false;
 }
 
-template <int GM, int UT>
+// The EMA update's bin select as the first `nblocks` blocks of the count
+// launch of et_route_update (BIN = true): blocks [0, nblocks) select (one
+// expert each, 1024 threads), the rest count tile blockIdx.x - nblocks.
+struct BinRole {
+    const uint32_t* partial;
+    uint32_t* bin;
+    uint32_t* rank;
+    float* bnd;
+    int nbx;
+    int nblocks;
+    uint32_t c;
+};
+
+template <int GM, int UT, bool BIN = false>
 __global__ __launch_bounds__(kMaxGpt<GM> * kWave, GM <= 2 ? 8 : 1) void route_pairs_kernel(
     const float* __restrict__ logits, const float* __restrict__ thr, int T, int E, int gpt,
     u32x2_t* __restrict__ pairs, uint8_t* __restrict__ group_counts, int32_t* __restrict__ group_slots,
-    int32_t* __restrict__ block_counts, int32_t* __restrict__ block_slots)
+    int32_t* __restrict__ block_counts, int32_t* __restrict__ block_slots, BinRole br)
 {
     constexpr int LC = kPairList<GM>;
     extern __shared__ float lds_f[];
+    int tile = (int)blockIdx.x;
+    if constexpr (BIN) {
+        static_assert(kMaxGpt<GM> * kWave == kSelectThreads, "the bin-select blocks fill the launch's blocks");
+        if (tile < br.nblocks) {
+            thr_bin_block(tile, br.nbx, br.partial, br.c, br.bin, br.rank, br.bnd);
+            return;
+        }
+        tile -= br.nblocks;
+        if ((int)threadIdx.x >= gpt * kWave) return;   // the tile's gpt waves count
+    }
     float* bth = lds_f;                      // [GM * 64] thresholds, by (group, lane)
     float* bhi = bth + GM * kWave;           // [GM * 64] logit bounds
     float* blo = bhi + GM * kWave;
@@ -728,7 +751,6 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave, GM <= 2 ? 8 : 1) void route_pa
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int G = (E + kWave - 1) / kWave;
-    const int tile = (int)blockIdx.x;
     const int64_t q = (int64_t)tile * gpt + wave;
     const int64_t t0 = q * kPairGroup;
     const int64_t t1 = std::min<int64_t>(T, t0 + kPairGroup);
@@ -890,26 +912,27 @@ __global__ __launch_bounds__(kScanThreads) void route_segscan_kernel(
                         seg_counts, block_slot_base, seg_slots);
 }
 
-// et_route_update's scan launch: blocks [0, E) run the EMA update's bin
-// select (one expert each), blocks E + seg * (G + 1) + gy the segmented scan.
-// Both only read what the count and histogram passes wrote, and each role
-// fills a 1024-thread block.
-static_assert(kScanThreads == kSelectThreads, "the scan and bin-select blocks have one size");
+// et_route_update's scan launch: blocks [0, ncol) run the EMA update's
+// collect pass (token block b % nbx of 64-expert group b / nbx), the rest the
+// segmented scan, block ncol + seg * (G + 1) + gy.  Both read only what earlier
+// launches wrote, and each role fills a 1024-thread block.
+static_assert(kScanThreads == kHistThreads, "the scan and collect blocks have one size");
 
-__global__ __launch_bounds__(kScanThreads) void upd_scan_bin_kernel(
-    int E, int nbx, const uint32_t* __restrict__ partial, uint32_t c, uint32_t* __restrict__ bin,
-    uint32_t* __restrict__ rank, float* __restrict__ bnd, const int32_t* __restrict__ block_counts,
-    const int32_t* __restrict__ block_slots, int NB, int RS, int32_t* __restrict__ block_base,
-    int32_t* __restrict__ seg_counts, int32_t* __restrict__ block_slot_base, int32_t* __restrict__ seg_slots)
+__global__ __launch_bounds__(kScanThreads) void upd_scan_collect_kernel(
+    int ncol, int nbx, const float* __restrict__ logits, int T, int E, int tpb, const uint32_t* __restrict__ bin,
+    const float* __restrict__ bnd, uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n,
+    const int32_t* __restrict__ block_counts, const int32_t* __restrict__ block_slots, int NB, int RS,
+    int32_t* __restrict__ block_base, int32_t* __restrict__ seg_counts, int32_t* __restrict__ block_slot_base,
+    int32_t* __restrict__ seg_slots)
 {
     const int b = (int)blockIdx.x;
-    if (b < E) {
-        thr_bin_block(b, nbx, partial, c, bin, rank, bnd);
+    if (b < ncol) {
+        thr_collect_block<kHistUT>(b % nbx, b / nbx, nbx, logits, T, E, tpb, bin, bnd, cand, cand_n);
         return;
     }
     const int G1 = (E + kWave - 1) / kWave + 1;
-    route_segscan_block((b - E) / G1, (b - E) % G1, block_counts, block_slots, NB, E, RS, block_base, seg_counts,
-                        block_slot_base, seg_slots);
+    route_segscan_block((b - ncol) / G1, (b - ncol) % G1, block_counts, block_slots, NB, E, RS, block_base,
+                        seg_counts, block_slot_base, seg_slots);
 }
 
 // Place kernel: block b = tile b; wave i handles the tile's route groups
@@ -1252,7 +1275,7 @@ static int pairs_count(const float* logits, const float* thr, int64_t T, int64_t
                            std::max(size_t(gpt) * kPairList<GM> * 8, size_t(gpt) * (E + 1) * 4);
         route_pairs_kernel<GM, UTM><<<dim3(NB), dim3(gpt * kWave), lds, s>>>(
             logits, thr, Ti, Ei, gpt, ws.pairs, ws.group_counts, ws.group_slots, ws.block_counts,
-            ws.block_slots);
+            ws.block_slots, BinRole{});
     });
     return check_launch("route_pairs_kernel");
 }
@@ -1292,23 +1315,39 @@ static int route_pairs_path(const float* logits, const float* thr, int64_t T, in
                        slot_capacity, p, ws, s);
 }
 
-int route_update_count(const float* logits, const float* thr, int64_t T, int64_t E, void* workspace,
-                       hipStream_t s)
+int route_update_count_bin(const float* logits, const float* thr, int64_t T, int64_t E, void* workspace,
+                           const uint32_t* partial, int nbx, uint32_t c, uint32_t* bin, uint32_t* rank,
+                           float* bnd, hipStream_t s)
 {
     const PairPlan p = pair_plan(T, E);
-    return pairs_count(logits, thr, T, E, p, pair_ws_layout(workspace, p, T, E), s);
+    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    if (p.G > 4) return fail(ET_ERR_INVALID_ARGUMENT, "route_update_count_bin: more than 256 experts");
+    const int Ti = (int)T, Ei = (int)E, gpt = (int)p.gpt, NB = (int)p.ntiles;
+    const BinRole br{partial, bin, rank, bnd, nbx, Ei, c};
+    ET_SWITCH_GROUPS(p.G, {
+        if constexpr (GM <= 4) {
+            const size_t lds = size_t(3 * GM * kWave) * 4 +
+                               std::max(size_t(gpt) * kPairList<GM> * 8, size_t(gpt) * (E + 1) * 4);
+            route_pairs_kernel<GM, kPairGroup, true><<<dim3(Ei + NB), dim3(kSelectThreads), lds, s>>>(
+                logits, thr, Ti, Ei, gpt, ws.pairs, ws.group_counts, ws.group_slots, ws.block_counts,
+                ws.block_slots, br);
+        }
+    });
+    return check_launch("route_pairs_kernel (with the bin select)");
 }
 
-int route_update_scan_bin(int64_t T, int64_t E, void* workspace, const uint32_t* partial, int nbx, uint32_t c,
-                          uint32_t* bin, uint32_t* rank, float* bnd, hipStream_t s)
+int route_update_scan_collect(int64_t T, int64_t E, void* workspace, const float* logits, int nbx, int tpb,
+                              const uint32_t* bin, const float* bnd, uint32_t* cand, uint32_t* cand_n,
+                              hipStream_t s)
 {
     const PairPlan p = pair_plan(T, E);
     const PairWs ws = pair_ws_layout(workspace, p, T, E);
     const int S = (int)p.nseg, RS = (int)p.seg_tiles;
-    upd_scan_bin_kernel<<<dim3((unsigned)(E + S * (p.G + 1))), dim3(kScanThreads), 0, s>>>(
-        (int)E, nbx, partial, c, bin, rank, bnd, ws.block_counts, ws.block_slots, (int)p.ntiles, RS, ws.block_base,
-        ws.seg_counts, ws.block_slot_base, ws.seg_slots);
-    return check_launch("upd_scan_bin_kernel");
+    const int ncol = nbx * p.G;
+    upd_scan_collect_kernel<<<dim3((unsigned)(ncol + S * (p.G + 1))), dim3(kScanThreads), 0, s>>>(
+        ncol, nbx, logits, (int)T, (int)E, tpb, bin, bnd, cand, cand_n, ws.block_counts, ws.block_slots,
+        (int)p.ntiles, RS, ws.block_base, ws.seg_counts, ws.block_slot_base, ws.seg_slots);
+    return check_launch("upd_scan_collect_kernel");
 }
 
 int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,

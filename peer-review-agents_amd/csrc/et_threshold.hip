@@ -183,45 +183,13 @@ __global__ __launch_bounds__(kHistThreads) void thr_hist_kernel(const float* __r
     hist_flush(h, partial);
 }
 
-// Collect pass: the keys in bin[e], into the block's segment of the expert's
-// list, cand[e][t0 + i] (i from an LDS counter, so i < t1 - t0); the block's
-// count goes to cand_n[e][block].  A logit at or below bnd[2e] scores below
-// the bin, one at or above bnd[2e + 1] above it; only the others (and NaN)
-// have their key evaluated.
 template <int UT>
 __global__ __launch_bounds__(kHistThreads) void thr_collect_kernel(
     const float* __restrict__ logits, int T, int E, int tpb, const uint32_t* __restrict__ bin,
     const float* __restrict__ bnd, uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n)
 {
-    __shared__ uint32_t cn[kWave];
-    const int tid = threadIdx.x;
-    if (tid < kWave) cn[tid] = 0u;
-    __syncthreads();
-    const int lane = lane_id();
-    const int wave = tid >> 6;
-    const int e = blockIdx.y * kWave + lane;
-    const bool ve = e < E;
-    const int ec = min(e, E - 1);
-    const uint32_t b1 = bin[ec];
-    const float lo = bnd[2 * ec], hi = bnd[2 * ec + 1];
-    const int64_t t0 = (int64_t)blockIdx.x * tpb;
-    const int64_t t1 = min((int64_t)T, t0 + tpb);
-    for (int64_t tb = t0 + (int64_t)wave * UT; tb < t1; tb += (int64_t)kHistWaves * UT) {
-        float v[UT];
-#pragma unroll
-        for (int u = 0; u < UT; ++u) v[u] = logits[min(tb + u, t1 - 1) * E + ec];
-#pragma unroll
-        for (int u = 0; u < UT; ++u) {
-            if (!ve || tb + u >= t1 || v[u] <= lo || v[u] >= hi) continue;
-            const uint32_t key = score_key(v[u]);
-            if (score_digit(key) == b1) {
-                const uint32_t i = atomicAdd(&cn[lane], 1u);
-                cand[(int64_t)e * T + t0 + i] = key;
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < kWave && ve) cand_n[(int64_t)e * gridDim.x + blockIdx.x] = cn[tid];
+    thr_collect_block<UT>((int)blockIdx.x, (int)blockIdx.y, (int)gridDim.x, logits, T, E, tpb, bin, bnd, cand,
+                          cand_n);
 }
 
 // The bin select's own kernel (thr_bin_block: et_threshold_internal.hpp).
@@ -432,27 +400,26 @@ extern "C" int et_route_update(const float* logits, float* thr, int64_t T, int64
     if (overlaps(route_workspace, rneed, thr_workspace, thr_ws_layout(nullptr, T, E).bytes))
         return fail(ET_ERR_INVALID_ARGUMENT, "et_route_update: the route and threshold workspaces overlap");
     // The routing reads thr before the update writes it: both on `stream`.
-    // On the pair-list path the routing's launches and the update's passes
-    // interleave, with the update's bin select in the routing scan's launch:
-    // count, histogram, scan + bin select, place, collect, final select.
+    // On the pair-list path (up to 256 experts) the update's passes run beside
+    // the routing's: histogram; count with the bin select; scan with the
+    // collect pass; place; final select.
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const ThrWs ws = thr_ws_layout(thr_workspace, T, E);
-    if (T > 0 && route_uses_pairs(T, E)) {
+    if (T > 0 && E <= 4 * kWave && route_uses_pairs(T, E)) {
         const unsigned groups = (unsigned)((E + kWave - 1) / kWave);
         const dim3 grid((unsigned)ws.g.blocks, groups);
         const int Ti = (int)T, Ei = (int)E, tpb = (int)ws.g.tpb, nb = (int)ws.g.blocks;
-        if (int rc = route_update_count(logits, thr, T, E, route_workspace, s)) return rc;
         thr_hist_kernel<kHistUT><<<grid, dim3(kHistThreads), 0, s>>>(logits, Ti, Ei, tpb, ws.partial);
         if (int rc = check_launch("thr_hist_kernel")) return rc;
-        if (int rc = route_update_scan_bin(T, E, route_workspace, ws.partial, nb,
-                                           (uint32_t)thr_rank(T, E, k_target), ws.bin, ws.rank, ws.bnd, s))
+        if (int rc = route_update_count_bin(logits, thr, T, E, route_workspace, ws.partial, nb,
+                                            (uint32_t)thr_rank(T, E, k_target), ws.bin, ws.rank, ws.bnd, s))
+            return rc;
+        if (int rc = route_update_scan_collect(T, E, route_workspace, logits, nb, tpb, ws.bin, ws.bnd, ws.cand,
+                                               ws.cand_n, s))
             return rc;
         if (int rc = route_update_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                                         token_slot, slot_capacity, route_workspace, s))
             return rc;
-        thr_collect_kernel<kHistUT><<<grid, dim3(kHistThreads), 0, s>>>(logits, Ti, Ei, tpb, ws.bin, ws.bnd,
-                                                                         ws.cand, ws.cand_n);
-        if (int rc = check_launch("thr_collect_kernel")) return rc;
         thr_final_kernel<<<dim3((unsigned)Ei), dim3(kSelectThreads), 0, s>>>(Ei, nb, Ti, tpb, ws.bin, ws.rank, ws.key,
                                                                             ws.cand, ws.cand_n, thr, stat, momentum);
         return check_launch("thr_final_kernel");

@@ -1,9 +1,9 @@
 // et_threshold_internal.hpp -- what the EMA threshold update shares with the
-// routing file: its digit constants and score keys, its bin select as a
-// per-block device function (run by its own kernel in et_threshold.hip and,
-// for et_route_update, beside the routing's segmented scan in et_route.hip),
-// and the routing launches that et_route_update interleaves with the
-// update's passes.  Not part of the C ABI.
+// routing file: its digit constants and score keys, its bin-select and
+// collect passes as per-block device functions (run by their own kernels in
+// et_threshold.hip and, for et_route_update, inside the routing's count and
+// scan launches in et_route.hip), and those routing launches.  Not part of the
+// C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -132,6 +132,49 @@ __device__ __forceinline__ void thr_bin_block(int e, int nblocks, const uint32_t
     }
 }
 
+// Collect pass: the keys in bin[e], into the block's segment of the expert's
+// list, cand[e][t0 + i] (i from an LDS counter, so i < t1 - t0); the block's
+// count goes to cand_n[e][block].  A logit at or below bnd[2e] scores below
+// the bin, one at or above bnd[2e + 1] above it; only the others (and NaN)
+// have their key evaluated.
+// Block (bx, by) of a grid of nbx token blocks by 64-expert groups, kHistThreads threads.
+template <int UT>
+__device__ __forceinline__ void thr_collect_block(int bx, int by, int nbx, const float* __restrict__ logits, int T,
+                                                  int E, int tpb, const uint32_t* __restrict__ bin,
+                                                  const float* __restrict__ bnd, uint32_t* __restrict__ cand,
+                                                  uint32_t* __restrict__ cand_n)
+{
+    __shared__ uint32_t cn[kWave];
+    const int tid = threadIdx.x;
+    if (tid < kWave) cn[tid] = 0u;
+    __syncthreads();
+    const int lane = lane_id();
+    const int wave = tid >> 6;
+    const int e = by * kWave + lane;
+    const bool ve = e < E;
+    const int ec = min(e, E - 1);
+    const uint32_t b1 = bin[ec];
+    const float lo = bnd[2 * ec], hi = bnd[2 * ec + 1];
+    const int64_t t0 = (int64_t)bx * tpb;
+    const int64_t t1 = min((int64_t)T, t0 + tpb);
+    for (int64_t tb = t0 + (int64_t)wave * UT; tb < t1; tb += (int64_t)kHistWaves * UT) {
+        float v[UT];
+#pragma unroll
+        for (int u = 0; u < UT; ++u) v[u] = logits[min(tb + u, t1 - 1) * E + ec];
+#pragma unroll
+        for (int u = 0; u < UT; ++u) {
+            if (!ve || tb + u >= t1 || v[u] <= lo || v[u] >= hi) continue;
+            const uint32_t key = score_key(v[u]);
+            if (score_digit(key) == b1) {
+                const uint32_t i = atomicAdd(&cn[lane], 1u);
+                cand[(int64_t)e * T + t0 + i] = key;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < kWave && ve) cand_n[(int64_t)e * nbx + bx] = cn[tid];
+}
+
 // The rank of the statistic: c = ceil(T * k_target / E), within [1, T].
 inline int64_t thr_rank(int64_t T, int64_t E, int64_t k_target)
 {
@@ -141,15 +184,18 @@ inline int64_t thr_rank(int64_t T, int64_t E, int64_t k_target)
     return c;
 }
 
-// et_route's three launches on the pair-list path (route_uses_pairs(T, E),
-// arguments and workspace already checked, T > 0), for et_route_update, which
-// puts the EMA update's histogram pass between the count and the scan, and
-// runs the update's bin select (over nbx histogram blocks per 64-expert
-// group, statistic rank c) in the scan's launch.
-int route_update_count(const float* logits, const float* thr, int64_t T, int64_t E, void* workspace,
-                       hipStream_t s);
-int route_update_scan_bin(int64_t T, int64_t E, void* workspace, const uint32_t* partial, int nbx, uint32_t c,
-                          uint32_t* bin, uint32_t* rank, float* bnd, hipStream_t s);
+// et_route's launches on the pair-list path (route_uses_pairs(T, E), at most
+// 256 experts, arguments and workspace already checked, T > 0), for
+// et_route_update, which runs the EMA update's passes beside them: its bin
+// select (over nbx histogram blocks per 64-expert group, statistic rank c) in
+// the count's launch, and its collect pass (token blocks of tpb tokens) in the
+// scan's.
+int route_update_count_bin(const float* logits, const float* thr, int64_t T, int64_t E, void* workspace,
+                           const uint32_t* partial, int nbx, uint32_t c, uint32_t* bin, uint32_t* rank,
+                           float* bnd, hipStream_t s);
+int route_update_scan_collect(int64_t T, int64_t E, void* workspace, const float* logits, int nbx, int tpb,
+                              const uint32_t* bin, const float* bnd, uint32_t* cand, uint32_t* cand_n,
+                              hipStream_t s);
 int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
                        int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
                        void* workspace, hipStream_t s);

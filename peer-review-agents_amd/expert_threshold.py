@@ -631,8 +631,7 @@ def route_update(logits: torch.Tensor, thr: torch.Tensor, k_target: int, momentu
     """Routing with the current thresholds, then the EMA update of thr from
     the same batch, in one call: the same results as :func:`route` followed by
     :func:`threshold_update_` (et_route_update), with every kernel on the
-    current stream and the routing scan and the update's bin select in one
-    launch."""
+    current stream and the update's small passes in the routing's launches."""
     _require(logits, "logits", torch.float32, 2)
     dev = logits.device
     T, E = logits.shape
