@@ -232,8 +232,8 @@ int et_threshold_update(const float* logits, float* thr, int64_t num_tokens, int
  * followed by et_threshold_update, bit for bit, with every kernel on
  * `stream`.  Where et_route takes its pair lists (up to 256 experts), the
  * update's small passes run in the routing's launches (histogram; count with
- * the bin select; scan with the collect pass; place; final select): five
- * launches for the two calls' seven.
+ * the bin select; scan with the collect pass; place with the final select):
+ * four launches for the two calls' seven (five below 32768 tokens).
  * Workspaces: route_workspace as et_route's, thr_workspace as
  * et_threshold_update's; their byte ranges must not overlap
  * (ET_ERR_INVALID_ARGUMENT).

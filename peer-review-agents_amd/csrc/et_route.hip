@@ -957,7 +957,26 @@ constexpr int kPlaceGroups = 2;
 constexpr int kStage = 2048;
 constexpr int kXcds = 8;           // accelerator complex dies of an MI355X
 
-template <int GM>
+// The EMA update's final select as the first blocks of the place launch of
+// et_route_update (FIN = true, tiles of kMaxGroupsPerTile groups): blocks
+// [0, E) select (one expert each, with the place blocks' kPlaceThreads
+// threads), blocks [E, nblocks) (to a multiple of 8) do nothing, and block
+// nblocks + i places the tiles that block i places without them.
+constexpr int kPlaceThreads = kMaxGroupsPerTile / 2 * kWave;   // 8 waves, 2 route groups each
+constexpr int kPairFinalKeys = 6144;   // candidates the paired final select holds in LDS
+struct FinalRole {
+    const uint32_t* bin;
+    const uint32_t* rank;
+    uint32_t* key;
+    const uint32_t* cand;
+    const uint32_t* cand_n;
+    float* thr;
+    float* stat;
+    float m;
+    int E, nblocks, nbx, T, tpb;
+};
+
+template <int GM, bool FIN = false>
 __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
     const u32x2_t* __restrict__ pairs, int T, int E, int gpt, int PG, int S, int RS,
     const int32_t* __restrict__ seg_counts, const int32_t* __restrict__ seg_slots,
@@ -965,18 +984,28 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
     const int32_t* __restrict__ group_slots, const int32_t* __restrict__ block_slot_base,
     const int32_t* __restrict__ block_counts, const int32_t* __restrict__ block_slots, int32_t* __restrict__ counts,
     int32_t* __restrict__ expert_offsets, int32_t* __restrict__ token_offsets, int32_t* __restrict__ sorted_token,
-    float* __restrict__ slot_gate, int32_t* __restrict__ token_slot, int64_t cap)
+    float* __restrict__ slot_gate, int32_t* __restrict__ token_slot, int64_t cap, FinalRole fr)
 {
     extern __shared__ int lds_i[];
+    if constexpr (FIN) {
+        static_assert(kMaxGpt<GM> * kWave / 2 == kPlaceThreads, "the final-select blocks fill the launch's blocks");
+        if ((int)blockIdx.x < fr.nblocks) {
+            if ((int)blockIdx.x < fr.E)
+                thr_final_block<kPlaceThreads, kPairFinalKeys>((int)blockIdx.x, fr.nbx, fr.T, fr.tpb, fr.bin, fr.rank,
+                                                               fr.key, fr.cand, fr.cand_n, fr.thr, fr.stat, fr.m,
+                                                               reinterpret_cast<uint32_t*>(lds_i));
+            return;
+        }
+    }
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     // Blocks go to the 8 XCDs in turn (block i to XCD i % 8).  With a whole
     // number of tiles per XCD, XCD x takes tiles [x n, (x + 1) n): its writes
     // to an expert's slots then form one contiguous range, whose cache lines
     // fill in that XCD's L2 instead of being written back in pieces by several.
-    const int nb = (int)gridDim.x;
-    const int b = (nb % kXcds == 0) ? ((int)blockIdx.x % kXcds) * (nb / kXcds) + (int)blockIdx.x / kXcds
-                                    : (int)blockIdx.x;
+    const int nb = (int)gridDim.x - (FIN ? fr.nblocks : 0);
+    const int bx = (int)blockIdx.x - (FIN ? fr.nblocks : 0);
+    const int b = (nb % kXcds == 0) ? (bx % kXcds) * (nb / kXcds) + bx / kXcds : bx;
     const int g0 = PG * wave;                       // the wave's first group within the tile
     const int G = (E + kWave - 1) / kWave;
     const int nwave = (int)blockDim.x / kWave;
@@ -1294,7 +1323,7 @@ static int pairs_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_of
         route_place_kernel<GM><<<dim3(NB), dim3(nwave * kWave), lds, s>>>(
             ws.pairs, Ti, Ei, gpt, PG, S, RS, ws.seg_counts, ws.seg_slots, ws.group_counts, ws.block_base,
             ws.group_slots, ws.block_slot_base, ws.block_counts, ws.block_slots, counts, expert_offsets,
-            token_offsets, sorted_token, slot_gate, token_slot, slot_capacity);
+            token_offsets, sorted_token, slot_gate, token_slot, slot_capacity, FinalRole{});
     });
     return check_launch("route_place_kernel");
 }
@@ -1348,6 +1377,41 @@ int route_update_scan_collect(int64_t T, int64_t E, void* workspace, const float
         ncol, nbx, logits, (int)T, (int)E, tpb, bin, bnd, cand, cand_n, ws.block_counts, ws.block_slots,
         (int)p.ntiles, RS, ws.block_base, ws.seg_counts, ws.block_slot_base, ws.seg_slots);
     return check_launch("upd_scan_collect_kernel");
+}
+
+bool route_update_pairs_final(int64_t T, int64_t E)
+{
+    const PairPlan p = pair_plan(T, E);
+    return p.G <= 4 && p.gpt == kMaxGroupsPerTile;
+}
+
+int route_update_place_final(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets,
+                             int32_t* token_offsets, int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                             int64_t slot_capacity, void* workspace, int nbx, int tpb, const uint32_t* bin,
+                             const uint32_t* rank, uint32_t* key, const uint32_t* cand, const uint32_t* cand_n,
+                             float* thr, float* stat, float m, hipStream_t s)
+{
+    const PairPlan p = pair_plan(T, E);
+    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    if (!route_update_pairs_final(T, E))
+        return fail(ET_ERR_INVALID_ARGUMENT, "route_update_place_final: tiles below 16 route groups");
+    const int Ti = (int)T, Ei = (int)E, gpt = (int)p.gpt, NB = (int)p.ntiles;
+    const int S = (int)p.nseg, RS = (int)p.seg_tiles;
+    const int nfin = (Ei + kXcds - 1) / kXcds * kXcds;
+    const FinalRole fr{bin, rank, key, cand, cand_n, thr, stat, m, Ei, nfin, nbx, Ti, tpb};
+    ET_SWITCH_GROUPS(p.G, {
+        if constexpr (GM <= 4) {
+            const int nwave = gpt / kPlaceGroups;
+            const size_t lds = std::max((size_t(gpt) * (E + 1) + 2 * size_t(E) + 2 + 2 * size_t(nwave) * E +
+                                         3 * kStage) * 4,
+                                        size_t(kFinalLdsWords<kPlaceThreads, kPairFinalKeys>) * 4);
+            route_place_kernel<GM, true><<<dim3(nfin + NB), dim3(kPlaceThreads), lds, s>>>(
+                ws.pairs, Ti, Ei, gpt, kPlaceGroups, S, RS, ws.seg_counts, ws.seg_slots, ws.group_counts,
+                ws.block_base, ws.group_slots, ws.block_slot_base, ws.block_counts, ws.block_slots, counts,
+                expert_offsets, token_offsets, sorted_token, slot_gate, token_slot, slot_capacity, fr);
+        }
+    });
+    return check_launch("route_place_kernel (with the final select)");
 }
 
 int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,

@@ -201,114 +201,15 @@ __global__ __launch_bounds__(kSelectThreads) void thr_bin_kernel(int E, int nblo
     thr_bin_block((int)blockIdx.x, nblocks, partial, c, bin, rank, bnd);
 }
 
-// Final select, one block per expert: the rank-th largest listed key.  The
-// bin's keys lie in [klo, khi] and share the bits above the highest bit in
-// which klo and khi differ; the rest are fixed 8 at a time from the top, each
-// round an LDS histogram of the next digit over the candidates that match the
-// bits fixed so far.  The candidate segments are walked up to kSelectThreads
-// at a time: a block-wide scan of their counts places them, and thread i of a
-// round finds its segment by binary search.  With at most kFinalLdsKeys
-// candidates the first walk copies them into LDS and every round reads them
-// there; otherwise every round walks the segments again.  Then the EMA; the
-// statistic's key is also left in key[e].
+// The final select's own kernel (thr_final_block: et_threshold_internal.hpp).
 __global__ __launch_bounds__(kSelectThreads) void thr_final_kernel(
     int E, int nblocks, int T, int tpb, const uint32_t* __restrict__ bin, const uint32_t* __restrict__ rank,
     uint32_t* __restrict__ key_out, const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_n,
     float* __restrict__ thr, float* __restrict__ stat, float m)
 {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t seg_end[kSelectThreads];  // inclusive scan of a round's segment counts
-    __shared__ uint32_t wsum[kSelectThreads / kWave];
-    __shared__ uint32_t sel[2];                  // the bits fixed so far and the rank inside them
-    __shared__ uint32_t ck[kFinalLdsKeys];
-    const int e = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const uint32_t b1 = bin[e];
-    const uint32_t klo = f2u(bin_edge(b1));
-    const uint32_t khi = b1 == (uint32_t)kBins - 1u ? f2u(1.0f) : f2u(bin_edge(b1 + 1u)) - 1u;
-    const uint32_t diff = klo ^ khi;
-    const int nbits = diff ? 32 - __builtin_clz(diff) : 0;   // at most 30
-    if (tid == 0) {
-        sel[0] = klo & ~((1u << nbits) - 1u);
-        sel[1] = rank[e];
-    }
-    const uint32_t* cl = cand + (int64_t)e * T;
-    const uint32_t* cnt = cand_n + (int64_t)e * nblocks;
-
-    // fn(i, key) for every listed key (i = its index in the concatenated list)
-    auto walk = [&](auto fn) {
-        uint32_t done = 0u;
-        for (int b0 = 0; b0 < nblocks; b0 += kSelectThreads) {
-            const int nc = min(kSelectThreads, nblocks - b0);
-            const uint32_t n = tid < nc ? cnt[b0 + tid] : 0u;
-            const uint32_t incl = (uint32_t)wave_incl_scan((int)n);
-            if (lane_id() == kWave - 1) wsum[wave] = incl;
-            __syncthreads();
-            uint32_t below = 0u;
-            for (int w = 0; w < wave; ++w) below += wsum[w];
-            seg_end[tid] = below + incl;
-            __syncthreads();
-            const uint32_t total = seg_end[nc - 1];
-            for (uint32_t i = tid; i < total; i += kSelectThreads) {
-                int lo = 0, hi = nc - 1;                 // the first segment that ends past i
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (seg_end[mid] > i) hi = mid; else lo = mid + 1;
-                }
-                const uint32_t start = lo ? seg_end[lo - 1] : 0u;
-                fn(done + i, cl[(int64_t)(b0 + lo) * tpb + (i - start)]);
-            }
-            done += total;
-            __syncthreads();
-        }
-        return done;
-    };
-    // the number of candidates, and a copy in LDS when they fit
-    __shared__ uint32_t n_all;
-    {
-        const uint32_t total = walk([&](uint32_t i, uint32_t k) {
-            if (i < (uint32_t)kFinalLdsKeys) ck[i] = k;
-        });
-        if (tid == 0) n_all = total;
-        __syncthreads();
-    }
-    const uint32_t total = n_all;
-    const bool in_lds = total <= (uint32_t)kFinalLdsKeys;
-    for (int sh = nbits; sh > 0; sh -= 8) {
-        const int lo_sh = sh > 8 ? sh - 8 : 0;
-        if (tid < 256) hist[tid] = 0u;
-        __syncthreads();
-        const uint32_t fixed = sel[0];
-        const uint32_t hmask = ~((1u << sh) - 1u);
-        const uint32_t dmask = (1u << (sh - lo_sh)) - 1u;
-        auto count = [&](uint32_t, uint32_t k) {
-            if ((k & hmask) == fixed) atomicAdd(&hist[(k >> lo_sh) & dmask], 1u);
-        };
-        if (in_lds) {
-            for (uint32_t i = tid; i < total; i += kSelectThreads) count(i, ck[i]);
-        } else {
-            walk(count);
-        }
-        __syncthreads();
-        if (tid < kWave) {
-            uint32_t b;
-            int rin;
-            if (find_digit<256>([&](int d) { return hist[d]; }, (int)sel[1], b, rin)) {
-                sel[0] = fixed | (b << lo_sh);
-                sel[1] = (uint32_t)rin;
-            }
-        }
-        __syncthreads();
-    }
-    if (tid != 0) return;
-    // every bit is fixed: sel[0] is the statistic's key
-    const uint32_t p = sel[0];
-    key_out[e] = p;
-    const float st = u2f(p);
-    if (stat) stat[e] = st;
-    const float one_minus_m = 1.0f - m;
-    thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
+    __shared__ uint32_t lds[kFinalLdsWords<kSelectThreads, kFinalLdsKeys>];
+    thr_final_block<kSelectThreads, kFinalLdsKeys>((int)blockIdx.x, nblocks, T, tpb, bin, rank, key_out, cand, cand_n,
+                                                   thr, stat, m, lds);
 }
 
 // The passes on stream s; the final select applies the EMA (and writes stat).
@@ -402,7 +303,8 @@ extern "C" int et_route_update(const float* logits, float* thr, int64_t T, int64
     // The routing reads thr before the update writes it: both on `stream`.
     // On the pair-list path (up to 256 experts) the update's passes run beside
     // the routing's: histogram; count with the bin select; scan with the
-    // collect pass; place; final select.
+    // collect pass; place with the final select (or place, then the final
+    // select, where the route tiles hold fewer than 16 groups).
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const ThrWs ws = thr_ws_layout(thr_workspace, T, E);
     if (T > 0 && E <= 4 * kWave && route_uses_pairs(T, E)) {
@@ -417,6 +319,10 @@ extern "C" int et_route_update(const float* logits, float* thr, int64_t T, int64
         if (int rc = route_update_scan_collect(T, E, route_workspace, logits, nb, tpb, ws.bin, ws.bnd, ws.cand,
                                                ws.cand_n, s))
             return rc;
+        if (route_update_pairs_final(T, E))
+            return route_update_place_final(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
+                                            token_slot, slot_capacity, route_workspace, nb, tpb, ws.bin, ws.rank,
+                                            ws.key, ws.cand, ws.cand_n, thr, stat, momentum, s);
         if (int rc = route_update_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                                         token_slot, slot_capacity, route_workspace, s))
             return rc;

@@ -1,9 +1,9 @@
 // et_threshold_internal.hpp -- what the EMA threshold update shares with the
-// routing file: its digit constants and score keys, its bin-select and
-// collect passes as per-block device functions (run by their own kernels in
-// et_threshold.hip and, for et_route_update, inside the routing's count and
-// scan launches in et_route.hip), and those routing launches.  Not part of the
-// C ABI.
+// routing file: its digit constants and score keys, its bin-select, collect
+// and final-select passes as per-block device functions (run by their own
+// kernels in et_threshold.hip and, for et_route_update, inside the routing's
+// count, scan and place launches in et_route.hip), and those routing
+// launches.  Not part of the C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -175,6 +175,120 @@ __device__ __forceinline__ void thr_collect_block(int bx, int by, int nbx, const
     if (tid < kWave && ve) cand_n[(int64_t)e * nbx + bx] = cn[tid];
 }
 
+// Final select, one block per expert: the rank-th largest listed key.  The
+// bin's keys lie in [klo, khi] and share the bits above the highest bit in
+// which klo and khi differ; the rest are fixed 8 at a time from the top, each
+// round an LDS histogram of the next digit over the candidates that match the
+// bits fixed so far.  The candidate segments are walked up to NT
+// at a time: a block-wide scan of their counts places them, and thread i of a
+// round finds its segment by binary search.  With at most KEYS
+// candidates the first walk copies them into LDS and every round reads them
+// there; otherwise every round walks the segments again.  Then the EMA; the
+// statistic's key is also left in key[e].  Block e of NT threads, whose LDS
+// (kFinalLdsWords<NT, KEYS> words at lds) holds up to KEYS candidates.
+template <int NT, int KEYS> constexpr int kFinalLdsWords = 256 + NT + NT / kWave + 3 + KEYS;
+
+template <int NT, int KEYS>
+__device__ __forceinline__ void thr_final_block(int e, int nblocks, int T, int tpb, const uint32_t* __restrict__ bin,
+                                                const uint32_t* __restrict__ rank, uint32_t* __restrict__ key_out,
+                                                const uint32_t* __restrict__ cand,
+                                                const uint32_t* __restrict__ cand_n, float* __restrict__ thr,
+                                                float* __restrict__ stat, float m, uint32_t* lds)
+{
+    uint32_t* hist = lds;                        // [256]
+    uint32_t* seg_end = hist + 256;              // [NT] inclusive scan of a round's segment counts
+    uint32_t* wsum = seg_end + NT;               // [NT / 64]
+    uint32_t* sel = wsum + NT / kWave;           // [2] the bits fixed so far and the rank inside them
+    uint32_t* n_all = sel + 2;                   // [1]
+    uint32_t* ck = n_all + 1;                    // [KEYS]
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const uint32_t b1 = bin[e];
+    const uint32_t klo = f2u(bin_edge(b1));
+    const uint32_t khi = b1 == (uint32_t)kBins - 1u ? f2u(1.0f) : f2u(bin_edge(b1 + 1u)) - 1u;
+    const uint32_t diff = klo ^ khi;
+    const int nbits = diff ? 32 - __builtin_clz(diff) : 0;   // at most 30
+    if (tid == 0) {
+        sel[0] = klo & ~((1u << nbits) - 1u);
+        sel[1] = rank[e];
+    }
+    const uint32_t* cl = cand + (int64_t)e * T;
+    const uint32_t* cnt = cand_n + (int64_t)e * nblocks;
+
+    // fn(i, key) for every listed key (i = its index in the concatenated list)
+    auto walk = [&](auto fn) {
+        uint32_t done = 0u;
+        for (int b0 = 0; b0 < nblocks; b0 += NT) {
+            const int nc = min(NT, nblocks - b0);
+            const uint32_t n = tid < nc ? cnt[b0 + tid] : 0u;
+            const uint32_t incl = (uint32_t)wave_incl_scan((int)n);
+            if (lane_id() == kWave - 1) wsum[wave] = incl;
+            __syncthreads();
+            uint32_t below = 0u;
+            for (int w = 0; w < wave; ++w) below += wsum[w];
+            seg_end[tid] = below + incl;
+            __syncthreads();
+            const uint32_t total = seg_end[nc - 1];
+            for (uint32_t i = tid; i < total; i += NT) {
+                int lo = 0, hi = nc - 1;                 // the first segment that ends past i
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (seg_end[mid] > i) hi = mid; else lo = mid + 1;
+                }
+                const uint32_t start = lo ? seg_end[lo - 1] : 0u;
+                fn(done + i, cl[(int64_t)(b0 + lo) * tpb + (i - start)]);
+            }
+            done += total;
+            __syncthreads();
+        }
+        return done;
+    };
+    // the number of candidates, and a copy in LDS when they fit
+    {
+        const uint32_t total = walk([&](uint32_t i, uint32_t k) {
+            if (i < (uint32_t)KEYS) ck[i] = k;
+        });
+        if (tid == 0) n_all[0] = total;
+        __syncthreads();
+    }
+    const uint32_t total = n_all[0];
+    const bool in_lds = total <= (uint32_t)KEYS;
+    for (int sh = nbits; sh > 0; sh -= 8) {
+        const int lo_sh = sh > 8 ? sh - 8 : 0;
+        if (tid < 256) hist[tid] = 0u;
+        __syncthreads();
+        const uint32_t fixed = sel[0];
+        const uint32_t hmask = ~((1u << sh) - 1u);
+        const uint32_t dmask = (1u << (sh - lo_sh)) - 1u;
+        auto count = [&](uint32_t, uint32_t k) {
+            if ((k & hmask) == fixed) atomicAdd(&hist[(k >> lo_sh) & dmask], 1u);
+        };
+        if (in_lds) {
+            for (uint32_t i = tid; i < total; i += NT) count(i, ck[i]);
+        } else {
+            walk(count);
+        }
+        __syncthreads();
+        if (tid < kWave) {
+            uint32_t b;
+            int rin;
+            if (find_digit<256>([&](int d) { return hist[d]; }, (int)sel[1], b, rin)) {
+                sel[0] = fixed | (b << lo_sh);
+                sel[1] = (uint32_t)rin;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    // every bit is fixed: sel[0] is the statistic's key
+    const uint32_t p = sel[0];
+    key_out[e] = p;
+    const float st = u2f(p);
+    if (stat) stat[e] = st;
+    const float one_minus_m = 1.0f - m;
+    thr[e] = __builtin_fmaf(m, thr[e], one_minus_m * st);
+}
+
 // The rank of the statistic: c = ceil(T * k_target / E), within [1, T].
 inline int64_t thr_rank(int64_t T, int64_t E, int64_t k_target)
 {
@@ -199,5 +313,14 @@ int route_update_scan_collect(int64_t T, int64_t E, void* workspace, const float
 int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets, int32_t* token_offsets,
                        int32_t* sorted_token, float* slot_gate, int32_t* token_slot, int64_t slot_capacity,
                        void* workspace, hipStream_t s);
+// Where the routing's tiles hold 16 route groups (T of at least 32768 tokens),
+// the place launch also runs the update's final select (over the collect
+// pass's nbx token blocks of tpb tokens), which applies the EMA to thr.
+bool route_update_pairs_final(int64_t T, int64_t E);
+int route_update_place_final(int64_t T, int64_t E, int32_t* counts, int32_t* expert_offsets,
+                             int32_t* token_offsets, int32_t* sorted_token, float* slot_gate, int32_t* token_slot,
+                             int64_t slot_capacity, void* workspace, int nbx, int tpb, const uint32_t* bin,
+                             const uint32_t* rank, uint32_t* key, const uint32_t* cand, const uint32_t* cand_n,
+                             float* thr, float* stat, float m, hipStream_t s);
 
 }  // namespace et

@@ -456,10 +456,13 @@ def _plans_identical(a, b):
 
 @pytest.mark.parametrize("T,E,k,cap", [(8192, 64, 8, None), (1, 4, 2, None), (5000, 128, 8, "under"),
                                        (131072, 64, 8, "exact"), (300, 1024, 16, None), (999, 7, 3, None),
-                                       (20000, 256, 8, None), (3, 65, 2, None), (4097, 200, 5, None)])
+                                       (20000, 256, 8, None), (3, 65, 2, None), (4097, 200, 5, None),
+                                       (32768, 1, 1, None), (40000, 256, 8, None), (50001, 200, 5, "under"),
+                                       (65536, 7, 3, None), (35000, 129, 4, "exact")])
 def test_route_update_matches_route_then_update(et, orc, dev, T, E, k, cap):
     """et_route_update equals route followed by threshold_update_ bit for
-    bit, and the oracle."""
+    bit, and the oracle.  From T = 32768 (route tiles of 16 groups) with at
+    most 256 experts the update's final select runs in the place launch."""
     print(f"route_update T={T} E={E} k={k} cap={cap}", flush=True)
     rng = np.random.default_rng([T, E, 5])
     lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
