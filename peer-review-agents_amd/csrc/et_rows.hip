@@ -461,9 +461,11 @@ static bool bwd_slot_order(int64_t T, int64_t cap, int64_t rb)
 // atomics: add and min, so the result does not depend on their order), scans
 // the counts, then places every slot.  Each thread loads kOrderBatch entries
 // before using any, so a window of up to kOrderThreads * kOrderBatch entries
-// pays one memory latency per pass.
+// pays one memory latency per pass.  Blocks past the nwin windows zero-fill
+// dlogits instead.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderBatch = 8;
+constexpr int kOrderZeroBlocks = 256;                // blocks of the order launch that zero-fill dlogits
 
 // Slots of token-list entries jb + k * kOrderThreads + threadIdx.x (k <
 // kOrderBatch) below j1, with their experts; -1 where out of range.
@@ -484,8 +486,22 @@ __device__ __forceinline__ void order_batch(const int32_t* __restrict__ tok_slot
 
 __global__ __launch_bounds__(kOrderThreads) void combine_bwd_order(
     const int32_t* __restrict__ tok_off, const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff,
-    int E, int T, int TW, int64_t cap, int32_t* __restrict__ order)
+    int E, int T, int TW, int64_t cap, int32_t* __restrict__ order, float* __restrict__ dlogits, int nwin)
 {
+    if ((int)blockIdx.x >= nwin) {
+        // The blocks past the windows zero-fill dlogits (16 bytes per thread a
+        // step), which pass 2 then writes at the routed entries: this launch
+        // occupies few CUs with its windows, so the fill costs no time here,
+        // where at the start of pass 1 it would take bandwidth from the rows.
+        const int64_t n4 = (int64_t)T * E / 4;
+        float4* d4 = reinterpret_cast<float4*>(dlogits);
+        const int64_t stride = (int64_t)(gridDim.x - nwin) * kOrderThreads;
+        for (int64_t i = (int64_t)(blockIdx.x - nwin) * kOrderThreads + threadIdx.x; i < n4; i += stride)
+            d4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (blockIdx.x == (unsigned)nwin && threadIdx.x == 0)
+            for (int64_t j = n4 * 4; j < (int64_t)T * E; ++j) dlogits[j] = 0.0f;
+        return;
+    }
     extern __shared__ int32_t sh[];                 // eo [E + 1], cnt [E], first [E]
     int32_t* eo = sh;
     int32_t* cnt = sh + E + 1;
@@ -548,15 +564,16 @@ __device__ __forceinline__ double fma_exact(float a, float b, double acc)
 }
 
 // The main pass: one wave per (J, pair of pieces); both pieces' loads are
-// issued before either is used.  The first waves in dispatch order also
-// zero-fill dlogits (1 KiB each), which pass 2 then writes at the routed
-// entries.
+// issued before either is used.  With zero_dl (no order launch did it) the
+// first waves in dispatch order also zero-fill dlogits (1 KiB each), which
+// pass 2 then writes at the routed entries.
 template <int DT>
 __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
     const char* __restrict__ dy, const char* __restrict__ yp, const float* __restrict__ gate,
     const int32_t* __restrict__ sorted_token, const int32_t* __restrict__ order,
     const int32_t* __restrict__ tok_slot, const int32_t* __restrict__ eoff, int E, int T, int64_t nch,
-    uint32_t npieces, int64_t cap, char* __restrict__ dyp, double* __restrict__ part, float* __restrict__ dlogits)
+    uint32_t npieces, int64_t cap, char* __restrict__ dyp, double* __restrict__ part, float* __restrict__ dlogits,
+    bool zero_dl)
 {
     using P = Pack<DT>;
     constexpr int N = P::N;
@@ -575,7 +592,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
     const int64_t rows = gridDim.x / kXcds;
     const int64_t x0 = (int64_t)(blockIdx.x % kXcds) * per;
     const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    if (dlogits) {
+    if (dlogits && zero_dl) {
         const int64_t n = (int64_t)T * E;
         const int64_t stride = (int64_t)gridDim.x * kBwdWaves * 4 * kWave;
         for (int64_t f = ((int64_t)blockIdx.x * kBwdWaves + wv) * 4 * kWave; f < n; f += stride)
@@ -974,10 +991,14 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
         char* wsb = static_cast<char*>(workspace);
         double* part = reinterpret_cast<double*>(wsb);
         int32_t* order = nullptr;
+        bool zero_here = true;                      // combine_bwd_vec zero-fills dlogits
         if (cap > 0 && !bwd_slot_order(T, cap, rb)) {
             order = reinterpret_cast<int32_t*>(wsb + bwd_order_offset(cap, bwd_parts(np)));
-            combine_bwd_order<<<dim3((unsigned)nw), dim3(kOrderThreads), (size_t)(3 * E + 1) * 4, s>>>(
-                token_offsets, token_slot, expert_offsets, (int)E, (int)T, (int)TW, cap, order);
+            // (blocks that zero-fill dlogits, where it is 16-byte aligned)
+            const int nz = (dlogits && (reinterpret_cast<uintptr_t>(dlogits) & 15) == 0) ? kOrderZeroBlocks : 0;
+            combine_bwd_order<<<dim3((unsigned)(nw + nz)), dim3(kOrderThreads), (size_t)(3 * E + 1) * 4, s>>>(
+                token_offsets, token_slot, expert_offsets, (int)E, (int)T, (int)TW, cap, order, dlogits, (int)nw);
+            zero_here = nz == 0;
             if (int rc = check_launch("combine_bwd_order")) return rc;
         }
         const size_t lds = (size_t)(E + 1) * 4;
@@ -991,7 +1012,7 @@ extern "C" int et_combine_bwd(const void* dy, const void* yp, const float* slot_
             const int64_t grid = (blocks + kXcds - 1) / kXcds * kXcds;
             ET_SWITCH_DT(dtype, combine_bwd_vec<DT><<<dim3((unsigned)grid), dim3(kBwdWaves * kWave), 0, s>>>(
                                     dyc, ypc, slot_gate, sorted_token, order, token_slot, expert_offsets, (int)E,
-                                    (int)T, nch, (uint32_t)np, cap, dypc, part, dlogits));
+                                    (int)T, nch, (uint32_t)np, cap, dypc, part, dlogits, zero_here));
             if (int rc = check_launch("combine_bwd_vec")) return rc;
         }
         if (cap == 0) return ET_OK;
