@@ -20,6 +20,11 @@
 // et_route_noalloc (the two-read path) keeps the older count / scan / fill
 // kernels, whose workspace is O(E) per block and fits a small static scratch:
 // the count and fill passes each read the logits, with lane = expert.
+// et_route_update (et_threshold.hip) runs the EMA update's bin select, collect
+// pass and final select as extra blocks of the count, scan and place launches
+// (route_pairs_kernel<..., true>, upd_scan_collect_kernel,
+// route_place_kernel<..., true>): a small pass beside a big one shares its
+// launch without slowing it.
 #include <algorithm>
 #include <mutex>
 

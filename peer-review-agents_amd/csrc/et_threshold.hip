@@ -32,6 +32,9 @@
 //     waves per block, lane = expert (coalesced row segments).  Counts are
 //     16-bit in LDS, two digits to a word, written whole to
 //     partial[group][block][lane][d / 2].
+// The bin-select, collect and final-select passes are block functions
+// (et_threshold_internal.hpp): et_threshold_update launches them as their own
+// kernels, et_route_update as extra blocks of the routing's launches.
 #include <algorithm>
 
 #include "et_common.hpp"
