@@ -110,7 +110,7 @@ def test_route_large_batch_takes_the_two_read_kernels(et, orc, dev):
     """T = 540000, E = 256: the pair lists would exceed 1 GiB, so et_route
     takes the count and fill kernels with a small workspace; routing still
     bit-exact with the oracle (quantile thresholds, NaN logits, fallback
-    tokens)."""
+    tokens), alone and in route_update (whose EMA update is bit-exact too)."""
     T, E = 540_000, 256
     print(f"route two-read T={T} E={E}", flush=True)
     assert et.route_workspace_bytes(T, E) < (64 << 20)
@@ -119,8 +119,17 @@ def test_route_large_batch_takes_the_two_read_kernels(et, orc, dev):
     lg[::9973] = -30.0                                   # tokens that clear no threshold
     lg[rng.random((T, E)) < 1e-4] = np.nan
     thr = np.full(E, 0.93, np.float32)
-    plan = et.route(dev_f32(lg, dev), dev_f32(thr, dev))
-    assert_route_equal(plan, orc.route(lg, thr))
+    L = dev_f32(lg, dev)
+    r = orc.route(lg, thr)
+    plan = et.route(L, dev_f32(thr, dev))
+    assert_route_equal(plan, r)
+    # route_update takes the same kernels, then the update's own passes
+    t = dev_f32(thr, dev)
+    stat = torch.empty(E, device=dev)
+    assert_route_equal(et.route_update(L, t, 8, 0.99, stat=stat), r)
+    thr_o, stat_o = orc.threshold_update(lg, thr, 8, 0.99)
+    np.testing.assert_array_equal(bits(host(stat)), bits(stat_o))
+    np.testing.assert_array_equal(bits(host(t)), bits(thr_o))
 
 
 def test_route_empty_batch(et, dev):
