@@ -83,7 +83,6 @@ constexpr int kWaitLgkm0 = 0xC07F;
 
 constexpr int kBM = 256;          // slots per tile
 constexpr int kBN = 256;          // output features per tile
-constexpr int kKC = 64;           // k per chunk (four k-steps of 16): 128 bytes of a row
 constexpr int kThreads = 256;
 // Slot tiles per group in the tile order: 8 for K >= 2048 (the gate/up
 // projections: 2.5-3% faster than 4 at C3 and C4), 4 below (the down
@@ -392,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void expert_gemm_kernel(GemmArgs g)
     // the K loop).
     // (gather mode keeps its 8 offsets in registers: reading the token from
     // LDS at each load would put an LDS wait before every load)
-    auto a_off = [&](const Tile& t, const Offsets& o, int i, int tb) -> uint32_t {
+    auto a_off = [&](const Tile& t, const Offsets& o, int i, [[maybe_unused]] int tb) -> uint32_t {
         const int R = 64 * wave + 8 * i + (lane >> 3);
         if constexpr (GATHER) {
             return o.a[i];

@@ -1185,11 +1185,11 @@ __global__ __launch_bounds__(kMaxGpt<GM> * kWave / 2) void route_place_kernel(
 // Expert-group bucket (GM) and tokens in flight per wave (UT = 32 / GM keeps
 // the logits of UT tokens x GM groups in 32 VGPRs).
 #define ET_SWITCH_GROUPS(G, ...)                                                            \
-    if ((G) <= 1) { constexpr int GM = 1, UT = 32; __VA_ARGS__; }                          \
-    else if ((G) <= 2) { constexpr int GM = 2, UT = 16; __VA_ARGS__; }                     \
-    else if ((G) <= 4) { constexpr int GM = 4, UT = 8; __VA_ARGS__; }                      \
-    else if ((G) <= 8) { constexpr int GM = 8, UT = 4; __VA_ARGS__; }                      \
-    else { constexpr int GM = 16, UT = 2; __VA_ARGS__; }
+    if ((G) <= 1) { constexpr int GM = 1, UT = 32; (void)UT; __VA_ARGS__; }                 \
+    else if ((G) <= 2) { constexpr int GM = 2, UT = 16; (void)UT; __VA_ARGS__; }            \
+    else if ((G) <= 4) { constexpr int GM = 4, UT = 8; (void)UT; __VA_ARGS__; }             \
+    else if ((G) <= 8) { constexpr int GM = 8, UT = 4; (void)UT; __VA_ARGS__; }             \
+    else { constexpr int GM = 16, UT = 2; (void)UT; __VA_ARGS__; }
 
 }  // namespace et
 
@@ -1275,7 +1275,7 @@ struct PairWs {
     size_t bytes;
 };
 
-static PairWs pair_ws_layout(void* base, const PairPlan& p, int64_t T, int64_t E)
+static PairWs pair_ws_layout(void* base, const PairPlan& p, int64_t E)
 {
     PairWs ws{};
     size_t off = 0;
@@ -1354,7 +1354,7 @@ int route_update_count_bin(const float* logits, const float* thr, int64_t T, int
                            float* bnd, hipStream_t s)
 {
     const PairPlan p = pair_plan(T, E);
-    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    const PairWs ws = pair_ws_layout(workspace, p, E);
     if (p.G > 4) return fail(ET_ERR_INVALID_ARGUMENT, "route_update_count_bin: more than 256 experts");
     const int Ti = (int)T, Ei = (int)E, gpt = (int)p.gpt, NB = (int)p.ntiles;
     const BinRole br{partial, bin, rank, bnd, nbx, Ei, c};
@@ -1375,7 +1375,7 @@ int route_update_scan_collect(int64_t T, int64_t E, void* workspace, const float
                               hipStream_t s)
 {
     const PairPlan p = pair_plan(T, E);
-    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    const PairWs ws = pair_ws_layout(workspace, p, E);
     const int S = (int)p.nseg, RS = (int)p.seg_tiles;
     const int ncol = nbx * p.G;
     upd_scan_collect_kernel<<<dim3((unsigned)(ncol + S * (p.G + 1))), dim3(kScanThreads), 0, s>>>(
@@ -1397,7 +1397,7 @@ int route_update_place_final(int64_t T, int64_t E, int32_t* counts, int32_t* exp
                              float* thr, float* stat, float m, hipStream_t s)
 {
     const PairPlan p = pair_plan(T, E);
-    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    const PairWs ws = pair_ws_layout(workspace, p, E);
     if (!route_update_pairs_final(T, E))
         return fail(ET_ERR_INVALID_ARGUMENT, "route_update_place_final: tiles below 16 route groups");
     const int Ti = (int)T, Ei = (int)E, gpt = (int)p.gpt, NB = (int)p.ntiles;
@@ -1425,7 +1425,7 @@ int route_update_place(int64_t T, int64_t E, int32_t* counts, int32_t* expert_of
 {
     const PairPlan p = pair_plan(T, E);
     return pairs_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate, token_slot,
-                       slot_capacity, p, pair_ws_layout(workspace, p, T, E), s);
+                       slot_capacity, p, pair_ws_layout(workspace, p, E), s);
 }
 
 }  // namespace et
@@ -1437,7 +1437,7 @@ using namespace et;
 // instead: the same outputs bit for bit, from a workspace of O(E) per block.
 constexpr size_t kPairWsLimit = size_t(1) << 30;
 
-static size_t pair_ws_bytes(int64_t T, int64_t E) { return pair_ws_layout(nullptr, pair_plan(T, E), T, E).bytes; }
+static size_t pair_ws_bytes(int64_t T, int64_t E) { return pair_ws_layout(nullptr, pair_plan(T, E), E).bytes; }
 static size_t two_read_ws_bytes(int64_t T, int64_t E) { return route_ws_layout(nullptr, route_plan(T, E), E).bytes; }
 static bool use_pairs(int64_t T, int64_t E) { return pair_ws_bytes(T, E) <= kPairWsLimit; }
 
@@ -1493,7 +1493,7 @@ extern "C" int et_route(const float* logits, const float* thr, int64_t T, int64_
         return route_two_read(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                               token_slot, slot_capacity, workspace, static_cast<hipStream_t>(stream));
     const PairPlan p = pair_plan(T, E);
-    const PairWs ws = pair_ws_layout(workspace, p, T, E);
+    const PairWs ws = pair_ws_layout(workspace, p, E);
     return route_pairs_path(logits, thr, T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                             token_slot, slot_capacity, p, ws, static_cast<hipStream_t>(stream));
 }

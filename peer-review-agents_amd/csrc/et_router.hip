@@ -67,7 +67,7 @@ template <> struct RtMfma<16> {
     }
     static __device__ __forceinline__ int crow(int lane, int j) { return 4 * (lane >> 4) + j; }
     // 16-token route group (within the wave) of element j of token tile m
-    static constexpr int group(int m, int j) { return m; }
+    static constexpr int group(int m, int /*j*/) { return m; }
 };
 template <> struct RtMfma<32> {
     static constexpr int KS = 16;

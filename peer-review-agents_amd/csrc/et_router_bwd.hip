@@ -242,9 +242,9 @@ __global__ __launch_bounds__(kThreads) void router_wgrad_kernel(
 #pragma unroll
             for (int u = 0; u < 2 * NC; ++u) read_half(0, 0, u >> 1, u & 1, bf[0][u >> 1]);
         }
-        // stage c, c & 1 == par: 4 k-steps x 2 NC slots
-        auto stage = [&](int c, auto parc) {
-            constexpr int par = decltype(parc)::value;
+        // stage c: 4 k-steps x 2 NC slots (the parity c & 1, as the second
+        // argument's type, gives each parity its own instantiation)
+        auto stage = [&](int c, auto /*parity*/) {
             constexpr int S = 8 * NC;
             refresh();
             if (A) set_bases(c);

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kHistThreads) void thr_collect_kernel(
 }
 
 // The bin select's own kernel (thr_bin_block: et_threshold_internal.hpp).
-__global__ __launch_bounds__(kSelectThreads) void thr_bin_kernel(int E, int nblocks,
+__global__ __launch_bounds__(kSelectThreads) void thr_bin_kernel(int nblocks,
                                                                  const uint32_t* __restrict__ partial, uint32_t c,
                                                                  uint32_t* __restrict__ bin,
                                                                  uint32_t* __restrict__ rank, float* __restrict__ bnd)
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(kSelectThreads) void thr_bin_kernel(int E, int nblo
 
 // The final select's own kernel (thr_final_block: et_threshold_internal.hpp).
 __global__ __launch_bounds__(kSelectThreads) void thr_final_kernel(
-    int E, int nblocks, int T, int tpb, const uint32_t* __restrict__ bin, const uint32_t* __restrict__ rank,
+    int nblocks, int T, int tpb, const uint32_t* __restrict__ bin, const uint32_t* __restrict__ rank,
     uint32_t* __restrict__ key_out, const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_n,
     float* __restrict__ thr, float* __restrict__ stat, float m)
 {
@@ -226,13 +226,13 @@ static int thr_passes(const float* logits, int64_t T, int64_t E, int64_t k_targe
     const int tpb = (int)ws.g.tpb, nb = (int)ws.g.blocks;
     thr_hist_kernel<kHistUT><<<grid, dim3(kHistThreads), 0, s>>>(logits, Ti, Ei, tpb, ws.partial);
     if (int rc = check_launch("thr_hist_kernel")) return rc;
-    thr_bin_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(Ei, nb, ws.partial, (uint32_t)c, ws.bin, ws.rank,
+    thr_bin_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(nb, ws.partial, (uint32_t)c, ws.bin, ws.rank,
                                                                ws.bnd);
     if (int rc = check_launch("thr_bin_kernel")) return rc;
     thr_collect_kernel<kHistUT><<<grid, dim3(kHistThreads), 0, s>>>(logits, Ti, Ei, tpb, ws.bin, ws.bnd, ws.cand,
                                                                      ws.cand_n);
     if (int rc = check_launch("thr_collect_kernel")) return rc;
-    thr_final_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(Ei, nb, Ti, tpb, ws.bin, ws.rank, ws.key, ws.cand,
+    thr_final_kernel<<<dim3(Ei), dim3(kSelectThreads), 0, s>>>(nb, Ti, tpb, ws.bin, ws.rank, ws.key, ws.cand,
                                                                 ws.cand_n, thr, stat, momentum);
     return check_launch("thr_final_kernel");
 }
@@ -329,7 +329,7 @@ extern "C" int et_route_update(const float* logits, float* thr, int64_t T, int64
         if (int rc = route_update_place(T, E, counts, expert_offsets, token_offsets, sorted_token, slot_gate,
                                         token_slot, slot_capacity, route_workspace, s))
             return rc;
-        thr_final_kernel<<<dim3((unsigned)Ei), dim3(kSelectThreads), 0, s>>>(Ei, nb, Ti, tpb, ws.bin, ws.rank, ws.key,
+        thr_final_kernel<<<dim3((unsigned)Ei), dim3(kSelectThreads), 0, s>>>(nb, Ti, tpb, ws.bin, ws.rank, ws.key,
                                                                             ws.cand, ws.cand_n, thr, stat, momentum);
         return check_launch("thr_final_kernel");
     }
