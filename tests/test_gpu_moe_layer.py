@@ -10,7 +10,6 @@ y = sum over routed (t, e) of gate * FFN_e(x_t).  Outputs and every gradient
 must agree within float32 rounding (relative to the magnitudes involved)."""
 import importlib
 
-import numpy as np
 import pytest
 import torch
 

@@ -7,7 +7,6 @@ torch.compile(fullgraph=True) -- so with no graph break -- and gives outputs,
 gradients and thresholds bit-identical to eager, over several steps."""
 import importlib
 
-import numpy as np
 import pytest
 import torch
 
