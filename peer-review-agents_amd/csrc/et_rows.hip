@@ -152,6 +152,17 @@ __device__ __forceinline__ void st16_nt(char* p, v4u v)
     __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(p));
 }
 
+// A non-temporal store at device scope (nt sc1): written through the XCD's L2
+// instead of being held there, so it leaves that L2 to the data a kernel
+// re-reads.  The compiler's non-temporal store has no scope bits, hence the
+// inline assembly.  The compiler's memory waits count only the operations it
+// issued itself; vector memory operations retire in issue order on gfx950, so
+// every wait it places for a load still covers that load.
+__device__ __forceinline__ void st16_nt_dev(char* p, v4u v)
+{
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+}
+
 // ---------------------------------------------------------------------------
 // dispatch forward: Xp[s] = X[t] for each slot s of t.  One wave per 1 KiB
 // piece of a token's row: each lane loads its 16-byte chunk once and stores it
@@ -404,7 +415,10 @@ __device__ __forceinline__ void load_eoff_lds(int* eoff_lds, const int32_t* __re
 // products in two chains (even and odd elements, then added), and one DPP
 // wave reduction sums the lanes, so the partial carries about a dozen
 // binary64 roundings.  Yp is read once and dYp written once, both
-// non-temporal.
+// non-temporal; the dYp stores also at device scope (nt sc1), which writes
+// them through the XCD's L2 and makes the pass about 1% faster at T = 65536,
+// d = 4096 (the L2 then holds less of a window's dY, which is fetched again
+// from beyond it more often, and still the pass is faster).
 //
 // Walk order.  Walking tokens (each token's ~k slots at once) has the waves in
 // flight touch a slot run in every expert block, each run visited again and
@@ -634,7 +648,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void combine_bwd_vec(
             P::unpack(wd[i], df);
 #pragma unroll
             for (int k = 0; k < N; ++k) o[k] = g * df[k];
-            if (on[i]) st16_nt(dyp + (int64_t)s * rb + idx[i] * 16, P::pack(o));
+            if (on[i]) st16_nt_dev(dyp + (int64_t)s * rb + idx[i] * 16, P::pack(o));
 #pragma unroll
             for (int k = 0; k < N; k += 2) {
                 a0 = fma_exact(df[k], f[k], a0);
