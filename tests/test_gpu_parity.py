@@ -325,6 +325,31 @@ def test_rows_token_windows(et, orc, dev, E, mode):
     assert torch.equal(dl_a.view(torch.int32), dl_b.view(torch.int32))
 
 
+@pytest.mark.parametrize("mode", ["quantile", "fallback"])
+@pytest.mark.parametrize("shift", [0, 1])
+def test_combine_backward_dlogits_into_used_buffer(et, orc, dev, mode, shift):
+    """dlogits written into a caller's buffer that holds NaN beforehand: every
+    entry that no routed pair sets must come back 0.  With the buffer 16-byte
+    aligned (shift 0) the token-window walk's order launch zero-fills it; one
+    float further on (shift 1) that launch leaves it alone and the main pass
+    zero-fills it.  Quantile routing takes the token windows (T = 1100,
+    d = 8192 bf16), fallback routing the plain slot order.  Either way every
+    routed entry equals dgate * (g * (1 - g)) bit for bit and every other
+    entry is 0 (no NaN left)."""
+    T, E, d = 1100, 24, 8192
+    print(f"combine_backward dlogits into a used buffer mode={mode} shift={shift}", flush=True)
+    lg, thr = synthetic_router(T, E, mode, seed=41)
+    r = orc.route(lg, thr)
+    x, yp, dy, _ = make_rows(orc, r, T, d, "bf16", 7)
+    plan = et.route(dev_f32(lg, dev), dev_f32(thr, dev))
+    buf = torch.full((T * E + shift,), float("nan"), dtype=torch.float32, device=dev)
+    out = buf[shift:].view(T, E)
+    assert (out.data_ptr() % 16 == 0) == (shift == 0)
+    _, dgate, dl = et.combine_backward(to_dev(dy, dev), to_dev(yp, dev), plan, out_dlogits=out)
+    assert dl.data_ptr() == out.data_ptr()
+    assert_dlogits(host(dl), host(dgate), r, E)
+
+
 @pytest.mark.parametrize("mode", ["fallback", "all", "special"])
 def test_rows_routing_modes(et, orc, dev, mode):
     lg, thr = synthetic_router(200, 24, mode, seed=9)
